@@ -1,0 +1,138 @@
+"""Seeded synthetic inputs shared by the golden generator, the tests and bench.py.
+
+Everything is drawn with ``numpy.random.RandomState`` (stable across numpy
+versions) and converted to bf16 / fp16 with torch's round-to-nearest-even
+casts, so a fixture's inputs can be regenerated anywhere from the seed alone.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+
+def bf16_bits(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16).copy()
+
+
+def outlier_activations(M: int, K: int, seed: int = 0, scale: float = 20.0, frac: float = 0.01,
+                        student_t: bool = False, dtype=torch.bfloat16) -> torch.Tensor:
+    """x ~ N(0,1) with round(frac*K) outlier channels.
+
+    ``student_t=False``: the outlier channels are multiplied by ``scale``
+    (the DiT-linear configuration).  ``student_t=True``: they are replaced by
+    Student-t(nu=3) draws (the heavy-tailed rotate+quant configuration).
+    """
+    rs = np.random.RandomState(seed)
+    x = rs.standard_normal((M, K)).astype(np.float32)
+    nout = int(round(frac * K))
+    ch = rs.choice(K, size=nout, replace=False)
+    if student_t:
+        x[:, ch] = rs.standard_t(3, size=(M, nout)).astype(np.float32)
+    else:
+        x[:, ch] *= scale
+    return torch.from_numpy(x).to(dtype)
+
+
+def normal_weight(N: int, K: int, seed: int = 1, std: float = 0.02, dtype=torch.float16) -> torch.Tensor:
+    rs = np.random.RandomState(seed)
+    return torch.from_numpy((rs.standard_normal((N, K)) * std).astype(np.float32)).to(dtype)
+
+
+def normal_bias(N: int, seed: int = 2, std: float = 0.01, dtype=torch.float16) -> torch.Tensor:
+    rs = np.random.RandomState(seed)
+    return torch.from_numpy((rs.standard_normal((N,)) * std).astype(np.float32)).to(dtype)
+
+
+def config1_x() -> torch.Tensor:
+    """x bf16 [256, 3072], N(0,1), 1% of channels x20, seed 0."""
+    return outlier_activations(256, 3072, seed=0)
+
+
+def config1_weight() -> torch.Tensor:
+    """W [3072, 3072] ~ N(0, 0.02) cast to fp16 (weights are quantized from fp16)."""
+    return normal_weight(3072, 3072, seed=1)
+
+
+def config1_bias() -> torch.Tensor:
+    return normal_bias(3072, seed=2)
+
+
+def hadamard_np(G: int) -> np.ndarray:
+    h4 = np.array([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=np.float64)
+    h = h4
+    while h.shape[0] < G:
+        h = np.kron(h, h4)
+    return h / np.sqrt(G)
+
+
+def preimage_rows(v: np.ndarray, G: int) -> np.ndarray:
+    """x = v @ H (float64); rotating x returns v exactly when x is representable."""
+    H = hadamard_np(G)
+    M, K = v.shape
+    return (v.reshape(M, K // G, G) @ H).reshape(M, K)
+
+
+def tie_rows(K: int = 256) -> torch.Tensor:
+    """bf16 rows whose exact rotation hits quantizer ties (x/s = k + 1/2)."""
+    G = 256
+    rows = []
+    # row 0: absmax 7 -> s = 1, values at every half-integer tie
+    v = np.zeros(K)
+    v[0] = 7.0
+    ties = [0.5, 1.5, 2.5, 3.5, 4.5, 5.5, 6.5]
+    for i, t in enumerate(ties):
+        v[1 + 2 * i] = t
+        v[2 + 2 * i] = -t
+    rows.append(v)
+    # row 1: absmax 3.5 -> s = 0.5, ties at (k+1/2)*0.5
+    v = np.zeros(K)
+    v[5] = 3.5
+    for i, t in enumerate(ties):
+        v[20 + i] = t * 0.5
+        v[40 + i] = -t * 0.5
+    rows.append(v)
+    v = np.stack(rows)
+    x = preimage_rows(v, G)
+    xt = torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16)
+    if not np.array_equal(xt.float().numpy().astype(np.float64), x):
+        raise AssertionError("tie preimage not representable in bf16")
+    return xt
+
+
+def edge_cases() -> dict:
+    """name -> (x tensor [M,K], convrot groupsize)."""
+    cases = {}
+    rs = np.random.RandomState(7)
+    # zero row, single nonzero, tiny row (hits the 1e-10 clamp), normal row
+    z = np.zeros((4, 256), dtype=np.float32)
+    z[1, 17] = 3.0
+    z[2, :] = rs.standard_normal(256).astype(np.float32) * 1e-12
+    z[3, :] = rs.standard_normal(256).astype(np.float32)
+    cases["zeros"] = (torch.from_numpy(z).to(torch.bfloat16), 256)
+    cases["ties"] = (tie_rows(), 256)
+    cases["g16"] = (torch.from_numpy(rs.standard_normal((8, 80)).astype(np.float32)).to(torch.bfloat16), 16)
+    cases["g64"] = (torch.from_numpy(rs.standard_normal((8, 192)).astype(np.float32)).to(torch.bfloat16), 64)
+    cases["f32"] = (torch.from_numpy(rs.standard_normal((8, 512)).astype(np.float32)), 256)
+    cases["f16"] = (torch.from_numpy(rs.standard_normal((8, 512)).astype(np.float32)).to(torch.float16), 256)
+    w = rs.standard_normal((4, 256)).astype(np.float32)
+    w[:, ::7] *= 1e-30                                  # >100 binades inside one group
+    w[:, 3] = 1e3
+    cases["wide_span"] = (torch.from_numpy(w).to(torch.bfloat16), 256)
+    cases["student_t"] = (outlier_activations(16, 1024, seed=3, student_t=True), 256)
+    return cases
+
+
+def stochastic_weight_case() -> torch.Tensor:
+    return normal_weight(64, 512, seed=11)
+
+
+def small_linear_case():
+    """Random packed codes over all byte values (nibble -8 included), scales U(0.005,0.05)."""
+    rs = np.random.RandomState(5)
+    M, N, K = 64, 48, 256
+    xp = torch.from_numpy(rs.randint(-128, 128, size=(M, K // 2)).astype(np.int8))
+    wp = torch.from_numpy(rs.randint(-128, 128, size=(N, K // 2)).astype(np.int8))
+    xs = torch.from_numpy(rs.uniform(0.005, 0.05, size=M).astype(np.float32))
+    ws = torch.from_numpy(rs.uniform(0.005, 0.05, size=N).astype(np.float32))
+    bias = torch.from_numpy((rs.standard_normal(N) * 0.01).astype(np.float32)).to(torch.float16)
+    return xp, wp, xs, ws, bias
