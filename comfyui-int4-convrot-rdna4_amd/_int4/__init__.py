@@ -1,0 +1,191 @@
+"""int4 ConvRot W4A4 backend for AMD MI355X (gfx950 / CDNA4).
+
+Drop-in for the reference backend package ``_int4`` (reference
+``_int4/__init__.py:9-13,35-42``): same public names, signatures, dtypes and
+exceptions, with every stage of the linear running in hand-written gfx950 HIP
+kernels (``csrc/``) reached through the C-ABI in ``native.py``.
+
+Public API:
+    quantize_convrot_w4a4_weight(weight, convrot_groupsize, ...) -> (qweight_i8, scale_f32)
+    dequantize_convrot_w4a4_weight(qdata, scales, convrot_groupsize, ...) -> tensor
+    convrot_w4a4_linear(x, qweight, wscales, bias, convrot_groupsize, ...) -> tensor
+    is_available() -> bool          # gfx950 ROCm device + loadable kernel library
+    pick_groupsize(in_features) -> int | None
+
+Numerics are those of the reference eager path (``_int4/eager.py``): packed
+codes and scales equal the eager ones, the integer accumulators are exact, and
+the epilogue is the fp32 chain fl32(fl32(fl32(acc*xs)*ws)+b) rounded once to
+the output dtype.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import native
+from ._codec import _INT4_GROUP_SIZE, _INT4_MAX, _pack_int4_row_major, _unpack_int4_row_major
+from .native import is_available as _native_available
+
+__all__ = [
+    "quantize_convrot_w4a4_weight",
+    "dequantize_convrot_w4a4_weight",
+    "convrot_w4a4_linear",
+    "convrot_w8a8_linear",
+    "is_available",
+    "pick_groupsize",
+]
+
+# dtypes the GEMM emits natively; others compute in fp32 then cast
+# (reference _int4/__init__.py:45)
+_NATIVE_OUT = frozenset({torch.float32, torch.bfloat16})
+
+
+def pick_groupsize(in_features: int) -> int | None:
+    """Largest supported ConvRot groupsize dividing in_features (256/64/16)
+    (reference _int4/__init__.py:69-74)."""
+    for g in (256, 64, 16):
+        if in_features % g == 0:
+            return g
+    return None
+
+
+def is_available() -> bool:
+    """True only on a gfx950 ROCm device with a loadable kernel library."""
+    return _native_available()
+
+
+def _check_groupsize(G: int) -> None:
+    if G < 4 or (G & (G - 1)) != 0 or math.log(G, 4) % 1 != 0:
+        raise ValueError(f"Regular Hadamard size must be a power of 4, got {G}")
+    if G not in (16, 64, 256):
+        raise ValueError(f"convrot_groupsize must be 16, 64 or 256, got {G}")
+
+
+def validate_w4a4_shape(tensor: torch.Tensor, convrot_groupsize: int, quant_group_size: int) -> None:
+    """reference _int4/eager.py:82-89"""
+    if tensor.dim() != 2:
+        raise ValueError(f"ConvRot W4A4 expects a 2D tensor, got shape {tuple(tensor.shape)}")
+    k = tensor.shape[-1]
+    if k % convrot_groupsize != 0:
+        raise ValueError(f"in_features {k} not divisible by convrot_groupsize {convrot_groupsize}")
+    if k % quant_group_size != 0:
+        raise ValueError(f"in_features {k} not divisible by quant_group_size {quant_group_size}")
+
+
+def _on_gpu(t: torch.Tensor) -> torch.Tensor:
+    if t.is_cuda:
+        return t
+    if not torch.cuda.is_available():
+        raise RuntimeError("the ConvRot int4 kernels need a gfx950 GPU; none is visible")
+    return t.to("cuda")
+
+
+def quantize_convrot_w4a4_weight(
+    weight: torch.Tensor,
+    convrot_groupsize: int = 256,
+    quant_group_size: int = _INT4_GROUP_SIZE,
+    stochastic_rounding: int | None = 0,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Rotate a weight with ConvRot and pack it as signed W4 (reference
+    _int4/eager.py:123-135).  Runs the fused gfx950 kernel in the weight's
+    dtype (the loader passes fp16, int4_ops.py:344-350).  Returns tensors on
+    the weight's device.
+
+    stochastic_rounding > 0 draws the rounding noise exactly as the reference
+    does (torch.rand with a generator seeded on the weight's device,
+    _int4/eager.py:92-101) and rounds with floor(t + u).
+    """
+    if quant_group_size != _INT4_GROUP_SIZE:
+        raise ValueError(f"int4 MMA kernel requires quant_group_size {_INT4_GROUP_SIZE}")
+    validate_w4a4_shape(weight, convrot_groupsize, quant_group_size)
+    _check_groupsize(convrot_groupsize)
+    dev = weight.device
+    w = _on_gpu(weight).contiguous()
+    if w.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        w = w.to(torch.float32)
+    if stochastic_rounding is not None and stochastic_rounding > 0:
+        gen = torch.Generator(device=weight.device)
+        gen.manual_seed(stochastic_rounding)
+        noise = torch.rand(weight.shape, dtype=w.dtype, layout=weight.layout, device=weight.device,
+                           generator=gen)
+        q, s = native.convrot_quant_int4_stochastic(w, convrot_groupsize, _on_gpu(noise))
+    else:
+        q, s = native.convrot_quant_int4(w, convrot_groupsize)
+    return q.to(dev), s.to(dev)
+
+
+def _hadamard(G: int, device, dtype=torch.float32) -> torch.Tensor:
+    """H_G = kron^(log4 G)(H4)/sqrt(G) (reference _int4/eager.py:20-46)."""
+    h4 = torch.tensor([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]],
+                      dtype=dtype, device=device)
+    h = h4
+    while h.shape[0] < G:
+        h = torch.kron(h, h4)
+    return h / (G ** 0.5)
+
+
+def dequantize_convrot_w4a4_weight(
+    qdata: torch.Tensor,
+    scales: torch.Tensor,
+    convrot_groupsize: int = 256,
+    quant_group_size: int = _INT4_GROUP_SIZE,
+    output_dtype: torch.dtype = torch.float32,
+) -> torch.Tensor:
+    """Dequantize packed ConvRot W4A4 weights and rotate back to the original
+    basis (reference _int4/eager.py:138-151).  A load-time / diagnostic helper,
+    not on the forward path; computed with torch ops in fp32."""
+    if quant_group_size != _INT4_GROUP_SIZE:
+        raise ValueError(f"int4 MMA kernel requires quant_group_size {_INT4_GROUP_SIZE}")
+    w = _unpack_int4_row_major(qdata).to(torch.float32)
+    w = w * scales.to(device=qdata.device, dtype=torch.float32).reshape(-1, 1)
+    N, K = w.shape
+    G = convrot_groupsize
+    h = _hadamard(G, qdata.device)
+    return torch.matmul(w.reshape(N, K // G, G), h.T).reshape(N, K).to(output_dtype)
+
+
+def convrot_w4a4_linear(
+    x: torch.Tensor,
+    qweight: torch.Tensor,
+    wscales: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    convrot_groupsize: int = 256,
+    quant_group_size: int = _INT4_GROUP_SIZE,
+    linear_dtype: str = "int4",
+) -> torch.Tensor:
+    """Compute ``x @ W.T + bias`` with the gfx950 W4A4 ConvRot path
+    (reference _int4/__init__.py:94-138).
+
+    Two kernels per call, both on torch's current stream: the fused
+    rotate+quantize of x, then the W4A4 GEMM with the dequant epilogue.  Every
+    row count takes the same kernels (the reference's torch-rotation branch
+    for M < 512 is not needed: the fused kernel is exact and fast at any M).
+    linear_dtype "int8" computes the same product (the reference routes it to
+    its eager path, whose arithmetic is identical).
+    """
+    if linear_dtype not in {"int4", "int8"}:
+        raise ValueError(f"ConvRot W4A4 linear_dtype must be 'int4' or 'int8', got {linear_dtype!r}")
+    if quant_group_size != _INT4_GROUP_SIZE:
+        raise ValueError(f"int4 MMA kernel requires quant_group_size {_INT4_GROUP_SIZE}")
+    if x.shape[-1] != qweight.shape[-1] * 2:
+        raise ValueError(f"Input K={x.shape[-1]} does not match qweight K={qweight.shape[-1] * 2}")
+    if x.shape[-1] % convrot_groupsize != 0:
+        raise ValueError(f"Input K={x.shape[-1]} not divisible by convrot_groupsize {convrot_groupsize}")
+    _check_groupsize(convrot_groupsize)
+
+    orig_shape = x.shape
+    x2d = x.reshape(-1, orig_shape[-1]).contiguous()
+    if x2d.dtype not in native._IN_DTYPE_CODE:
+        x2d = x2d.to(torch.float32)
+    qact, x_scale = native.convrot_quant_int4(x2d, convrot_groupsize)
+    out_dtype = x.dtype if x.dtype in _NATIVE_OUT else torch.float32
+    out = native.int4_convrot_gemm(qact, qweight, x_scale, wscales, bias, out_dtype)
+    if out.dtype != x.dtype:
+        out = out.to(x.dtype)
+    return out.reshape(*orig_shape[:-1], qweight.shape[0])
+
+
+def convrot_w8a8_linear(x, qweight, wscales, bias=None, convrot_groupsize=256):
+    """W8A8 tier (reference _int4/__init__.py:141-175): not built for gfx950 yet."""
+    raise NotImplementedError("the ConvRot W8A8 tier has no gfx950 kernels in this build")

@@ -1,0 +1,214 @@
+"""ctypes binding of libconvrot_gfx950.so (replaces the reference's
+``_int4/hip_loader.py`` + JIT ``_int4/build.py``).
+
+Same wrapper names, argument meaning and error behaviour as the reference
+loader (``_int4/hip_loader.py:74-92`` ``convrot_quant_int4``,
+``:158-207`` ``int4_convrot_gemm``, ``:150-155`` ``is_available``): outputs are
+allocated here with torch, the work is enqueued on torch's current stream, a
+nonzero return code raises ``RuntimeError``.  The library is prebuilt for
+gfx950 (``build.py``); a missing library raises instead of building or falling
+back to anything else.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+from . import build as _build
+
+_lib = None
+_lock = threading.Lock()
+
+# dtype codes of the C-ABI (reference _int4/hip_loader.py:38-39)
+_DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1}
+_IN_DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+EPI_F32, EPI_BF16, EPI_BF16_EAGER, EPI_ACC = 0, 1, 2, 3
+
+_vp, _i = ctypes.c_void_p, ctypes.c_int
+_SIGNATURES = {
+    "ck_convrot_quant_int4": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
+    "ck_int4_convrot_gemm": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
+    "cr_int4_convrot_gemm_ex": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
+    "cr_convrot_quant_int4_stochastic": ([_vp, _i, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
+    "cr_max_quant_k": ([], _i),
+    "cr_abi_version": ([], _i),
+}
+
+
+def lib_path() -> str:
+    return _build.lib_path()
+
+
+def load_library():
+    """Load (once) and return the ctypes handle.  Loaded after torch so the
+    library binds to the HIP runtime torch already mapped."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = lib_path()
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"{os.path.basename(path)} is not built; run the package's _int4/build.py "
+                "(hipcc --offload-arch=gfx950) first")
+        lib = ctypes.CDLL(path)
+        for name, (args, res) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = lib
+    return _lib
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def _is_gfx950() -> bool:
+    if getattr(torch.version, "hip", None) is None or not torch.cuda.is_available():
+        return False
+    try:
+        arch = (torch.cuda.get_device_properties(0).gcnArchName or "").split(":")[0]
+    except Exception:
+        return False
+    return arch == "gfx950"
+
+
+def is_available() -> bool:
+    """True only on a gfx950 ROCm device with the library loadable."""
+    if not _is_gfx950():
+        return False
+    try:
+        load_library()
+        return True
+    except Exception:
+        return False
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _check_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(f"expected a CUDA (HIP) tensor, got device {t.device}")
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous and 16-byte aligned (the kernels use 128-bit loads/stores)."""
+    t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def max_quant_k() -> int:
+    return int(load_library().cr_max_quant_k())
+
+
+def convrot_quant_int4(x: torch.Tensor, convrot_groupsize: int):
+    """Fused ConvRot rotation + rowwise int4 quantize (reference hip_loader.py:74-92).
+
+    Returns (qpacked int8 [M, K/2], scale f32 [M]).  Supports groupsize 16/64/256.
+    """
+    lib = load_library()
+    if convrot_groupsize not in (16, 64, 256):
+        raise ValueError("fused convrot_quant_int4 supports groupsize 16/64/256")
+    if x.dtype not in _IN_DTYPE_CODE:
+        raise ValueError(f"convrot_quant_int4 input dtype must be f32/bf16/f16, got {x.dtype}")
+    _check_cuda(x)
+    x = _aligned(x)
+    M, K = x.shape
+    qout = torch.empty((M, K // 2), dtype=torch.int8, device=x.device)
+    scale = torch.empty((M,), dtype=torch.float32, device=x.device)
+    rc = lib.ck_convrot_quant_int4(_ptr(x), _IN_DTYPE_CODE[x.dtype], _ptr(qout), _ptr(scale),
+                                   M, K, convrot_groupsize, _stream(x.device))
+    if rc != 0:
+        raise RuntimeError(f"ck_convrot_quant_int4 failed, hipError={rc}")
+    return qout, scale
+
+
+def convrot_quant_int4_stochastic(x: torch.Tensor, convrot_groupsize: int, noise: torch.Tensor):
+    """Rotation + int4 quantize with stochastic rounding q = floor(t + u)."""
+    lib = load_library()
+    if convrot_groupsize not in (16, 64, 256):
+        raise ValueError("fused convrot_quant_int4 supports groupsize 16/64/256")
+    if x.dtype not in _IN_DTYPE_CODE or noise.dtype != x.dtype or noise.shape != x.shape:
+        raise ValueError("noise must match x in shape and dtype")
+    _check_cuda(x, noise)
+    x = _aligned(x)
+    noise = noise.contiguous()
+    M, K = x.shape
+    qout = torch.empty((M, K // 2), dtype=torch.int8, device=x.device)
+    scale = torch.empty((M,), dtype=torch.float32, device=x.device)
+    rc = lib.cr_convrot_quant_int4_stochastic(_ptr(x), _IN_DTYPE_CODE[x.dtype], _ptr(noise), _ptr(qout),
+                                              _ptr(scale), M, K, convrot_groupsize, _stream(x.device))
+    if rc != 0:
+        raise RuntimeError(f"cr_convrot_quant_int4_stochastic failed, hipError={rc}")
+    return qout, scale
+
+
+def _gemm_args(x_packed, w_packed, x_scale, w_scale, bias):
+    _check_cuda(x_packed, w_packed, x_scale, w_scale, bias)
+    x_packed = _aligned(x_packed)
+    w_packed = _aligned(w_packed)
+    if x_packed.dtype != torch.int8 or w_packed.dtype != torch.int8:
+        raise ValueError("packed operands must be int8")
+    M, Kp = x_packed.shape
+    N, Kp2 = w_packed.shape
+    if Kp != Kp2:
+        raise ValueError(f"K mismatch: x {tuple(x_packed.shape)} w {tuple(w_packed.shape)}")
+    x_scale = x_scale.to(torch.float32).contiguous() if x_scale is not None else None
+    w_scale = w_scale.to(torch.float32).contiguous() if w_scale is not None else None
+    if bias is not None:
+        bias = bias.to(torch.float32).contiguous()
+    return x_packed, w_packed, x_scale, w_scale, bias, M, N, 2 * Kp
+
+
+def int4_convrot_gemm_ex(x_packed, w_packed, x_scale, w_scale, bias, epilogue: int):
+    """out = epilogue(sum_k qx qw, x_scale, w_scale, bias); see include/convrot_mi355x.h."""
+    lib = load_library()
+    x_packed, w_packed, x_scale, w_scale, bias, M, N, K = _gemm_args(
+        x_packed, w_packed, x_scale, w_scale, bias)
+    odt = {EPI_F32: torch.float32, EPI_BF16: torch.bfloat16, EPI_BF16_EAGER: torch.bfloat16,
+           EPI_ACC: torch.int32}[epilogue]
+    out = torch.empty((M, N), dtype=odt, device=x_packed.device)
+    rc = lib.cr_int4_convrot_gemm_ex(_ptr(x_packed), _ptr(w_packed), _ptr(x_scale), _ptr(w_scale),
+                                     _ptr(bias), _ptr(out), M, N, K, epilogue, _stream(x_packed.device))
+    if rc != 0:
+        raise RuntimeError(f"cr_int4_convrot_gemm_ex failed, hipError={rc}")
+    return out
+
+
+def int4_gemm_acc(x_packed, w_packed):
+    """Exact int32 accumulators acc[m, n] = sum_k qx[m,k] * qw[n,k]."""
+    return int4_convrot_gemm_ex(x_packed, w_packed, None, None, None, EPI_ACC)
+
+
+def int4_convrot_gemm(x_packed, w_packed, x_scale, w_scale, bias, out_dtype):
+    """out[M,N] = (Xint @ Wint^T) * x_scale[:,None] * w_scale[None,:] (+ bias)
+    (reference hip_loader.py:158-207, without its split-K branch: the gfx950
+    kernel fills the device at every shape that path served)."""
+    if out_dtype not in _DTYPE_CODE:
+        raise ValueError(f"hip int4 gemm output dtype must be float32/bfloat16, got {out_dtype}")
+    lib = load_library()
+    x_packed, w_packed, x_scale, w_scale, bias, M, N, K = _gemm_args(
+        x_packed, w_packed, x_scale, w_scale, bias)
+    out = torch.empty((M, N), dtype=out_dtype, device=x_packed.device)
+    rc = lib.ck_int4_convrot_gemm(_ptr(x_packed), _ptr(w_packed), _ptr(x_scale), _ptr(w_scale),
+                                  _ptr(bias), _ptr(out), M, N, K, _DTYPE_CODE[out_dtype],
+                                  _stream(x_packed.device))
+    if rc != 0:
+        raise RuntimeError(f"ck_int4_convrot_gemm failed, hipError={rc}")
+    return out

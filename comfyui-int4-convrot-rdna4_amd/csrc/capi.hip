@@ -1,0 +1,64 @@
+// extern "C" boundary of libconvrot_gfx950.so; declarations and contracts in
+// include/convrot_mi355x.h.
+
+#include "../../include/convrot_mi355x.h"
+#include "common.h"
+
+namespace convrot {
+hipError_t rotquant_launch(const void* x, int in_dtype, const void* noise, int8_t* q, float* s,
+                           int M, int K, int G, hipStream_t st);
+int rotquant_max_k();
+hipError_t gemm_launch(const int8_t* Xp, const int8_t* Wp, const float* xs, const float* ws,
+                       const float* bias, void* out, int M, int N, int K, int epi, hipStream_t st);
+}  // namespace convrot
+
+#define API extern "C" __attribute__((visibility("default")))
+
+static int quant_args_ok(int in_dtype, int M, int K, int G) {
+    if (!(G == 16 || G == 64 || G == 256)) return 0;
+    if (M < 0 || K <= 0 || K % G != 0) return 0;
+    if (K > convrot::rotquant_max_k()) return 0;
+    if (in_dtype < 0 || in_dtype > 2) return 0;
+    return 1;
+}
+
+API int ck_convrot_quant_int4(const void* x, int in_dtype, void* qout, void* scaleout,
+                              int M, int K, int G, void* stream) {
+    if (!quant_args_ok(in_dtype, M, K, G)) return -1;
+    hipError_t e = convrot::rotquant_launch(x, in_dtype, nullptr, reinterpret_cast<int8_t*>(qout),
+                                            reinterpret_cast<float*>(scaleout), M, K, G,
+                                            reinterpret_cast<hipStream_t>(stream));
+    return (int)e;
+}
+
+API int cr_convrot_quant_int4_stochastic(const void* x, int in_dtype, const void* noise, void* qout,
+                                         void* scaleout, int M, int K, int G, void* stream) {
+    if (!quant_args_ok(in_dtype, M, K, G) || noise == nullptr) return -1;
+    hipError_t e = convrot::rotquant_launch(x, in_dtype, noise, reinterpret_cast<int8_t*>(qout),
+                                            reinterpret_cast<float*>(scaleout), M, K, G,
+                                            reinterpret_cast<hipStream_t>(stream));
+    return (int)e;
+}
+
+API int cr_int4_convrot_gemm_ex(const void* Xp, const void* Wp, const void* xscale, const void* wscale,
+                                const void* bias, void* out, int M, int N, int K, int epilogue,
+                                void* stream) {
+    if (K % 32 != 0 || K <= 0 || K >= 131072 || M < 0 || N < 0) return -1;
+    if (epilogue < 0 || epilogue > 3) return -1;
+    hipError_t e = convrot::gemm_launch(reinterpret_cast<const int8_t*>(Xp), reinterpret_cast<const int8_t*>(Wp),
+                                        reinterpret_cast<const float*>(xscale), reinterpret_cast<const float*>(wscale),
+                                        reinterpret_cast<const float*>(bias), out, M, N, K, epilogue,
+                                        reinterpret_cast<hipStream_t>(stream));
+    return (int)e;
+}
+
+API int ck_int4_convrot_gemm(const void* Xp, const void* Wp, const void* xscale, const void* wscale,
+                             const void* bias, void* out, int M, int N, int K, int out_dtype,
+                             void* stream) {
+    if (out_dtype != 0 && out_dtype != 1) return -1;
+    return cr_int4_convrot_gemm_ex(Xp, Wp, xscale, wscale, bias, out, M, N, K, out_dtype, stream);
+}
+
+API int cr_max_quant_k(void) { return convrot::rotquant_max_k(); }
+
+API int cr_abi_version(void) { return 1; }

@@ -1,0 +1,57 @@
+// Shared device helpers for the gfx950 W4A4 ConvRot kernels.
+#pragma once
+
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace convrot {
+
+// dtype codes of the C-ABI (reference: _int4/hip_loader.py:38-39)
+enum : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
+
+__device__ __forceinline__ float bf16lo_to_f32(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi_to_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ float f16bits_to_f32(uint32_t h) {
+    return __half2float(__ushort_as_half((unsigned short)(h & 0xffffu)));
+}
+
+// float -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    return (uint32_t)__bfloat16_as_ushort(__float2bfloat16(f));
+}
+
+// Round a float once to the element dtype and widen it back (RNE).
+template <int DT>
+__device__ __forceinline__ float round_to_dt(float f) {
+    if constexpr (DT == DT_BF16) {
+        return __uint_as_float(f32_to_bf16_bits(f) << 16);
+    } else if constexpr (DT == DT_F16) {
+        return __half2float(__float2half_rn(f));
+    } else {
+        return f;
+    }
+}
+
+// Round an fp64 value ONCE to the element dtype (RNE), returned as float.
+// bf16 / f16: the low 32 bits of the double are folded into a sticky bit at
+// mantissa bit 32 ("jamming"); the result then has at most 21 significant bits
+// and converts to float exactly, and the single float -> dtype rounding sees
+// the same guard bit and the same sticky predicate as the exact value, so it
+// rounds the same way.  f32: one fp64 -> fp32 conversion.
+template <int DT>
+__device__ __forceinline__ float round_f64_to_dt(double d) {
+    if constexpr (DT == DT_F32) {
+        return (float)d;
+    } else {
+        uint64_t u = (uint64_t)__double_as_longlong(d);
+        uint32_t hi = (uint32_t)(u >> 32), lo = (uint32_t)u;
+        hi |= (lo != 0u) ? 1u : 0u;
+        float f = (float)__longlong_as_double((long long)((uint64_t)hi << 32));
+        return round_to_dt<DT>(f);
+    }
+}
+
+}  // namespace convrot

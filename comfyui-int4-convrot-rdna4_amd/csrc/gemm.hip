@@ -1,0 +1,205 @@
+// W4A4 GEMM with int32 accumulation and a fused dequant epilogue (gfx950).
+//
+//   acc[m, n] = sum_k qx[m, k] * qw[n, k]          (signed nibbles, exact int32)
+//   out[m, n] = epilogue(acc, xs[m], ws[n], bias[n])
+//
+// Inputs are the reference's packed layout (_int4/_codec.py:19-25): row-major
+// int8 [rows, K/2], element 2j in the low nibble of byte j, element 2j+1 in
+// the high nibble.  Semantics follow _int4/eager.py:154-169 (int4_linear).
+//
+// CDNA4 has no int4 matrix instruction, so nibbles become int8 operands of
+// v_mfma_i32_32x32x32_i8.  The unpack needs no sign extension: for a packed
+// dword w, (w & 0xF0F0F0F0) holds 16 * q(odd k) in every byte and
+// ((w << 4) & 0xF0F0F0F0) holds 16 * q(even k), both exact signed int8
+// (16 * -8 = -128).  The MFMA therefore accumulates 256 * acc, which stays
+// below 2^31 for K < 131072, and an arithmetic shift by 8 recovers acc.  The
+// k order inside one MFMA does not matter as long as A and B use the same
+// permutation, which they do (same loads, same unpack).
+//
+// Tiling: a 512-lane workgroup computes a 256 x 256 tile; its 8 waves form a
+// 2 (M) x 4 (N) grid of 128 x 64 wave tiles (4 x 2 MFMA 32x32 tiles).  Packed
+// nibbles are staged through LDS in 128-k blocks (64 bytes per row, rows
+// padded to 80 bytes so every 8-lane phase of a ds_read_b128 hits distinct
+// banks), double-buffered, one barrier per block.
+
+#include "common.h"
+
+namespace convrot {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+enum : int { EPI_F32 = 0, EPI_BF16 = 1, EPI_BF16_EAGER = 2, EPI_ACC = 3 };
+
+constexpr int TBM = 256, TBN = 256;  // workgroup tile
+constexpr int TBK = 128;             // k values per LDS block
+constexpr int ROWB = TBK / 2;        // packed bytes per row per block (64)
+constexpr int LDS_STRIDE = 80;       // padded row stride in bytes
+constexpr int NTHR = 512;
+constexpr int WTM = 128, WTN = 64;   // wave tile
+constexpr int FM = WTM / 32, FN = WTN / 32;
+
+__device__ __forceinline__ void unpack16(uint4 p, v4i& lo_step, v4i& hi_step) {
+    // 32 nibbles -> two MFMA operands of 16 int8 each (16 * q)
+    lo_step = (v4i){(int)((p.x << 4) & 0xF0F0F0F0u), (int)(p.x & 0xF0F0F0F0u),
+                    (int)((p.y << 4) & 0xF0F0F0F0u), (int)(p.y & 0xF0F0F0F0u)};
+    hi_step = (v4i){(int)((p.z << 4) & 0xF0F0F0F0u), (int)(p.z & 0xF0F0F0F0u),
+                    (int)((p.w << 4) & 0xF0F0F0F0u), (int)(p.w & 0xF0F0F0F0u)};
+}
+
+__device__ __forceinline__ float bf16r(float f) { return round_to_dt<DT_BF16>(f); }
+
+template <int EPI>
+__global__ __launch_bounds__(NTHR) void w4a4_gemm_kernel(
+        const int8_t* __restrict__ Xp, const int8_t* __restrict__ Wp,
+        const float* __restrict__ xs, const float* __restrict__ ws, const float* __restrict__ bias,
+        void* __restrict__ out, int M, int N, int K) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2][(TBM + TBN) * LDS_STRIDE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 2;            // 0..1
+    const int wn = wave & 3;             // 0..3
+    const int m0 = blockIdx.y * TBM;
+    const int n0 = blockIdx.x * TBN;
+    const int Kb = K / 2;                // packed bytes per row
+    const int nkb = (K + TBK - 1) / TBK;
+
+    // global -> LDS staging: (TBM + TBN) rows x 4 chunks of 16 B = 2048 chunks, 4 per lane
+    uint4 stage[4];
+    auto gload = [&](int kb) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int id = tid + j * NTHR;          // 0..2047
+            const int r = id >> 2;                  // 0..511 (A rows then B rows)
+            const int c16 = id & 3;
+            const int kbyte = kb * ROWB + c16 * 16;
+            uint4 v = make_uint4(0u, 0u, 0u, 0u);
+            if (r < TBM) {
+                const int gm = m0 + r;
+                if (gm < M && kbyte < Kb)
+                    v = *reinterpret_cast<const uint4*>(Xp + (size_t)gm * Kb + kbyte);
+            } else {
+                const int gn = n0 + (r - TBM);
+                if (gn < N && kbyte < Kb)
+                    v = *reinterpret_cast<const uint4*>(Wp + (size_t)gn * Kb + kbyte);
+            }
+            stage[j] = v;
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int id = tid + j * NTHR;
+            const int r = id >> 2;
+            const int c16 = id & 3;
+            *reinterpret_cast<uint4*>(&lds[buf][r * LDS_STRIDE + c16 * 16]) = stage[j];
+        }
+    };
+
+    v16i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = (v16i){0};
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+
+    const int frow = lane & 31;          // fragment row within a 32-row tile
+    const int fhalf = lane >> 5;         // which 16-byte half of a 32-byte k slice
+
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int buf = kb & 1;
+        if (kb + 1 < nkb) gload(kb + 1);
+        const uint8_t* la = &lds[buf][0];
+        const uint8_t* lb = &lds[buf][TBM * LDS_STRIDE];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {            // two 64-k slices per block
+            const int koff = s2 * 32 + fhalf * 16;
+            v4i a_lo[FM], a_hi[FM], b_lo[FN], b_hi[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const uint4 p = *reinterpret_cast<const uint4*>(la + (wm * WTM + i * 32 + frow) * LDS_STRIDE + koff);
+                unpack16(p, a_lo[i], a_hi[i]);
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const uint4 p = *reinterpret_cast<const uint4*>(lb + (wn * WTN + j * 32 + frow) * LDS_STRIDE + koff);
+                unpack16(p, b_lo[j], b_hi[j]);
+            }
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_lo[i], b_lo[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_hi[i], b_hi[j], acc[i][j], 0, 0, 0);
+                }
+        }
+        if (kb + 1 < nkb) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    // epilogue: 32x32 accumulator layout, lane l / register r ->
+    //   col = l % 32, row = 8 * (r / 4) + 4 * (l / 32) + r % 4
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int col = n0 + wn * WTN + j * 32 + (lane & 31);
+            if (col >= N) continue;
+            float wsc = 0.0f, bv = 0.0f;
+            if constexpr (EPI != EPI_ACC) {
+                wsc = ws[col];
+                if (bias) bv = bias[col];
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (row >= M) continue;
+                const int a = acc[i][j][r] >> 8;
+                const size_t o = (size_t)row * N + col;
+                if constexpr (EPI == EPI_ACC) {
+                    reinterpret_cast<int32_t*>(out)[o] = a;
+                } else if constexpr (EPI == EPI_BF16_EAGER) {
+                    float v = bf16r(bf16r((float)a) * bf16r(xs[row]));
+                    v = bf16r(v * bf16r(wsc));
+                    if (bias) v = bf16r(v + bf16r(bv));
+                    reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f32_to_bf16_bits(v);
+                } else {
+                    float v = __fmul_rn(__fmul_rn((float)a, xs[row]), wsc);
+                    if (bias) v = __fadd_rn(v, bv);
+                    if constexpr (EPI == EPI_F32) reinterpret_cast<float*>(out)[o] = v;
+                    else reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f32_to_bf16_bits(v);
+                }
+            }
+        }
+    }
+}
+
+hipError_t gemm_launch(const int8_t* Xp, const int8_t* Wp, const float* xs, const float* ws,
+                       const float* bias, void* out, int M, int N, int K, int epi, hipStream_t st) {
+    if (M == 0 || N == 0) return hipSuccess;
+    dim3 grid((N + TBN - 1) / TBN, (M + TBM - 1) / TBM), block(NTHR);
+    switch (epi) {
+        case EPI_F32:
+            hipLaunchKernelGGL(w4a4_gemm_kernel<EPI_F32>, grid, block, 0, st, Xp, Wp, xs, ws, bias, out, M, N, K);
+            break;
+        case EPI_BF16:
+            hipLaunchKernelGGL(w4a4_gemm_kernel<EPI_BF16>, grid, block, 0, st, Xp, Wp, xs, ws, bias, out, M, N, K);
+            break;
+        case EPI_BF16_EAGER:
+            hipLaunchKernelGGL(w4a4_gemm_kernel<EPI_BF16_EAGER>, grid, block, 0, st, Xp, Wp, xs, ws, bias, out, M, N, K);
+            break;
+        case EPI_ACC:
+            hipLaunchKernelGGL(w4a4_gemm_kernel<EPI_ACC>, grid, block, 0, st, Xp, Wp, xs, ws, bias, out, M, N, K);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace convrot

@@ -1,0 +1,328 @@
+// Fused ConvRot rotation + rowwise int4 quantization + nibble packing (gfx950).
+//
+// Computes, for every row of x [M, K] (dtype DT) and convrot block size G:
+//   xr  = RNE_DT( x_g @ H_G )          exactly rounded block-Hadamard rotation
+//   a   = max(max_k |xr|, DT(1e-10))
+//   s   = RNE_DT( fl32(a / 7) )        -> scale[m] (float)
+//   q   = rint_even( RNE_DT( fl32(xr / s) ) )   (or the stochastic variant)
+//   out = nibble pack, even k in the low nibble
+// which is the arithmetic of the reference eager path
+// (_int4/eager.py:65-79 rotation, :104-120 quantizer, _int4/_codec.py:19-25
+// pack).  Nothing here follows the reference RDNA4 kernel
+// (_int4/int4_gemm.hip:348-408), whose fp32-reciprocal arithmetic differs.
+//
+// Work layout
+//   * A lane owns a "chunk" of 16 consecutive elements (32 B of bf16, two
+//     16-byte loads).  Chunks of one row are spread over `tpr` lanes; when a
+//     row has more than 256 chunks a lane takes NPASS chunks (passes).
+//   * The 16 elements cover two base-4 digits (d0, d1) of the Hadamard index,
+//     so the first two radix-4 stages run in registers.  For G = 64 / 256 the
+//     remaining digit(s) live across 4 / 16 lanes; one LDS transpose of the
+//     fp64 partial sums brings them into registers for the last stage(s).
+//   * Every butterfly runs in fp64.  A group's partial sums are integer
+//     multiples of its smallest input ulp bounded by G * max|x|, so they are
+//     exact whenever the group's nonzero inputs span at most 53 - 8 - 2*log4(G)
+//     - 1 binades (bf16; 36 for G = 256), which real activations satisfy by a
+//     wide margin.  The exact value is then rounded once to DT.
+//   * The row absmax is reduced through an LDS atomic max; codes go through
+//     an LDS byte buffer so each lane stores 8 contiguous packed bytes.
+//
+// Quantizer exactness.  xr and s are values of DT (p = 8 significant bits for
+// bf16, 11 for f16).  Their quotient mx/ms * 2^d is never a DT rounding
+// midpoint (that needs an odd (p+1)-bit numerator, while odd(mx)/odd(ms) has
+// at most p bits) and lies at least 2^-(2p+1) (relative) from every midpoint.
+// So any approximation P of xr/s with relative error below that distance has
+// RNE_DT(P) == RNE_DT(xr/s) == RNE_DT(fl32(xr/s)):
+//   bf16: P = fl32(xr * fl32(1/s)), error <= 2^-23 < 2^-17;
+//   f16:  P = fl32(fl64(xr * fl64(1/s))), error <= 2^-24 + 2^-52 < 2^-23.
+// f32 uses the IEEE fp32 division directly.
+
+#include "common.h"
+
+namespace convrot {
+
+constexpr int kChunk = 16;       // elements per lane per pass
+constexpr int kMaxThreads = 256; // lanes per workgroup
+constexpr int kPad = 17;         // fp64 words per lane slot in the transpose buffer
+
+// radix-4 stage of the regular Hadamard H4 on four values:
+// H4 v = (sum v) 1 - 2 reverse(v)   (H4 as in _int4/eager.py:32-36)
+__device__ __forceinline__ void h4_stage(double& a, double& b, double& c, double& d, double scale) {
+    double S = ((a + b) + (c + d)) * scale;
+    double t = 2.0 * scale;
+    double na = S - t * d, nb = S - t * c, nc = S - t * b, nd = S - t * a;
+    a = na; b = nb; c = nc; d = nd;
+}
+
+// stage over one base-4 digit of the 16-entry register array (stride 1 or 4)
+template <int STRIDE>
+__device__ __forceinline__ void stage16(double (&v)[16], double scale) {
+#pragma unroll
+    for (int base = 0; base < 16; ++base) {
+        if ((base / STRIDE) % 4 != 0) continue;
+        h4_stage(v[base], v[base + STRIDE], v[base + 2 * STRIDE], v[base + 3 * STRIDE], scale);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void load_chunk(const void* __restrict__ x, size_t elem, double (&v)[16]) {
+    if constexpr (DT == DT_F32) {
+        const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(x) + elem);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint4 w = p[q];
+            v[4 * q + 0] = (double)__uint_as_float(w.x);
+            v[4 * q + 1] = (double)__uint_as_float(w.y);
+            v[4 * q + 2] = (double)__uint_as_float(w.z);
+            v[4 * q + 3] = (double)__uint_as_float(w.w);
+        }
+    } else {
+        const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(x) + elem);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            uint4 w4 = p[q];
+            uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if constexpr (DT == DT_BF16) {
+                    v[8 * q + 2 * j] = (double)bf16lo_to_f32(w[j]);
+                    v[8 * q + 2 * j + 1] = (double)bf16hi_to_f32(w[j]);
+                } else {
+                    v[8 * q + 2 * j] = (double)f16bits_to_f32(w[j]);
+                    v[8 * q + 2 * j + 1] = (double)f16bits_to_f32(w[j] >> 16);
+                }
+            }
+        }
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ float load_scalar(const void* __restrict__ p, size_t i) {
+    if constexpr (DT == DT_F32) return reinterpret_cast<const float*>(p)[i];
+    else if constexpr (DT == DT_BF16) return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(p)[i] << 16);
+    else return f16bits_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+
+// the python scalar 1e-10 of the eager clamp, converted to the tensor dtype
+template <int DT>
+__device__ __forceinline__ float clamp_floor() {
+    if constexpr (DT == DT_F32) return 1e-10f;
+    else if constexpr (DT == DT_BF16) return __uint_as_float(0x2edc0000u);  // bf16(1e-10)
+    else return 0.0f;                                                        // f16(1e-10) underflows
+}
+
+// group-local element index held in register slot i after the last stage,
+// for lane position gl within the group (see the transpose below)
+template <int G>
+__device__ __forceinline__ int final_elem(int gl, int i) {
+    if constexpr (G == 256) return gl + 16 * i;
+    else if constexpr (G == 64) return 16 * (i >> 2) + 4 * gl + (i & 3);
+    else return i;
+}
+
+template <int DT, int G, int NPASS, bool STOCH>
+__global__ __launch_bounds__(kMaxThreads) void rotquant_kernel(
+        const void* __restrict__ x, const void* __restrict__ noise,
+        int8_t* __restrict__ qout, float* __restrict__ sout,
+        int M, int K, int tpr, int rows_per_wg) {
+    constexpr int LPG = G / kChunk;             // lanes per convrot group
+    __shared__ double tbuf[kMaxThreads * kPad];
+    __shared__ uint32_t cbuf[kMaxThreads * 4];  // 16 code bytes per lane slot
+    __shared__ uint32_t rowmax[kMaxThreads];
+
+    const int tid = threadIdx.x;
+    const int rloc = tid / tpr;
+    const int t = tid - rloc * tpr;
+    const int row = blockIdx.x * rows_per_wg + rloc;
+    const bool row_ok = (rloc < rows_per_wg) && (row < M);
+    const int nchunks = K / kChunk;
+    const int gl = t % LPG;                     // lane position inside its group
+    const int gfirst = tid - gl;                // workgroup slot of the group's first lane
+
+    if (tid < rows_per_wg) rowmax[tid] = 0u;
+
+    float xr[NPASS][kChunk];
+    float lmax = 0.0f;
+
+#pragma unroll
+    for (int p = 0; p < NPASS; ++p) {
+        const int c = p * tpr + t;
+        const bool ok = row_ok && (c < nchunks);
+        double v[16];
+        if (ok) {
+            load_chunk<DT>(x, (size_t)row * K + (size_t)c * kChunk, v);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = 0.0;
+        }
+        // digits d0 (stride 1) and d1 (stride 4) in registers
+        if constexpr (G == 16) {
+            stage16<1>(v, 1.0);
+            stage16<4>(v, 0.25);                // 1/sqrt(16), exact
+        } else {
+            stage16<1>(v, 1.0);
+            stage16<4>(v, 1.0);
+            // transpose across the LPG lanes of the group through LDS
+            __syncthreads();                    // previous pass finished reading
+#pragma unroll
+            for (int i = 0; i < 16; ++i) tbuf[tid * kPad + i] = v[i];
+            __syncthreads();
+            if constexpr (G == 256) {
+                // lane gl takes position gl of every lane's 16: w[m] = (d0d1 = gl, d2d3 = m)
+#pragma unroll
+                for (int m = 0; m < 16; ++m) v[m] = tbuf[(gfirst + m) * kPad + gl];
+                stage16<1>(v, 1.0);
+                stage16<4>(v, 1.0 / 16.0);      // 1/sqrt(256), exact
+            } else {                            // G == 64, LPG == 4
+                // w[a + 4 b] = (d0d1 = 4 gl + a, d2 = b)
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+#pragma unroll
+                    for (int a = 0; a < 4; ++a) v[a + 4 * b] = tbuf[(gfirst + b) * kPad + 4 * gl + a];
+                stage16<4>(v, 1.0 / 8.0);       // 1/sqrt(64), exact
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float r = round_f64_to_dt<DT>(v[i]);
+            xr[p][i] = r;
+            if (ok) lmax = fmaxf(lmax, fabsf(r));
+        }
+    }
+
+    // row absmax (non-negative floats order like their bit patterns)
+    __syncthreads();
+    if (row_ok) atomicMax(&rowmax[rloc], __float_as_uint(lmax));
+    __syncthreads();
+
+    float a = __uint_as_float(row_ok ? rowmax[rloc] : 0u);
+    a = fmaxf(a, clamp_floor<DT>());
+    const float s = round_to_dt<DT>(a / 7.0f);  // IEEE division (no fast-math)
+    if (row_ok && t == 0) sout[row] = s;
+    const double rinv = 1.0 / (double)s;
+    const float rinv32 = 1.0f / s;
+    const float kMagic = 12582912.0f;           // 1.5 * 2^23: float add rounds to integer, ties to even
+
+#pragma unroll
+    for (int p = 0; p < NPASS; ++p) {
+        const int c = p * tpr + t;
+        const bool ok = row_ok && (c < nchunks);
+        const int gbase = (c - gl) * kChunk;    // group's first element within the row
+        uint8_t codes[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float z;
+            if constexpr (DT == DT_F32) z = xr[p][i] / s;
+            else if constexpr (DT == DT_BF16) z = round_to_dt<DT>(xr[p][i] * rinv32);
+            else z = round_to_dt<DT>((float)((double)xr[p][i] * rinv));
+            int q;
+            if constexpr (STOCH) {
+                const int e = final_elem<G>(gl, i);
+                float u = ok ? load_scalar<DT>(noise, (size_t)row * K + gbase + e) : 0.0f;
+                float f = floorf(round_to_dt<DT>(z + u));
+                f = fminf(fmaxf(f, -7.0f), 7.0f);
+                q = (f == f) ? (int)f : 0;      // NaN (0/0 when s == 0) -> 0
+            } else {
+                // f16 rows of zeros have s == 0 and give 0/0: the code is 0
+                if constexpr (DT == DT_F16) z = (z == z) ? z : 0.0f;
+                z = fminf(fmaxf(z, -7.0f), 7.0f);       // |z| <= 7.02 already; guards non-finite input
+                q = (int)__float_as_uint(z + kMagic);   // low nibble = rint_even(z)
+            }
+            codes[i] = (uint8_t)(q & 0xF);
+        }
+        // scatter codes to their element positions, then read back own chunk
+        __syncthreads();
+        uint8_t* cb = reinterpret_cast<uint8_t*>(cbuf);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int e = final_elem<G>(gl, i);
+            cb[(gfirst + e / kChunk) * 16 + (e % kChunk)] = codes[i];
+        }
+        __syncthreads();
+        if (ok) {
+            const uint4 w = reinterpret_cast<const uint4*>(cbuf)[tid];
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+            uint32_t o[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint32_t t0 = ws[2 * h] | (ws[2 * h] >> 4);
+                uint32_t t1 = ws[2 * h + 1] | (ws[2 * h + 1] >> 4);
+                o[h] = (t0 & 0xffu) | ((t0 >> 8) & 0xff00u) | ((t1 & 0xffu) << 16) | ((t1 << 8) & 0xff000000u);
+            }
+            uint2* dst = reinterpret_cast<uint2*>(qout + (size_t)row * (K / 2) + (size_t)c * (kChunk / 2));
+            *dst = make_uint2(o[0], o[1]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host-side launch
+// ---------------------------------------------------------------------------
+
+struct RQPlan { int npass, tpr, rows_per_wg, grid, block; };
+
+static inline int rq_plan(int M, int K, int G, RQPlan* pl) {
+    const int lpg = G / kChunk;
+    const int nchunks = K / kChunk;
+    int npass = (nchunks + kMaxThreads - 1) / kMaxThreads;
+    if (npass < 1) npass = 1;
+    int tpr = (nchunks + npass - 1) / npass;
+    tpr = ((tpr + lpg - 1) / lpg) * lpg;
+    if (tpr > kMaxThreads) return -1;
+    int rpw = (npass == 1) ? kMaxThreads / tpr : 1;
+    if (rpw < 1) rpw = 1;
+    if (rpw > M) rpw = M > 0 ? M : 1;
+    pl->npass = npass; pl->tpr = tpr; pl->rows_per_wg = rpw;
+    pl->grid = (M + rpw - 1) / rpw;
+    pl->block = rpw * tpr;
+    return 0;
+}
+
+template <int DT, int G, bool STOCH>
+static hipError_t rq_launch_g(const void* x, const void* noise, int8_t* q, float* s, int M, int K,
+                              hipStream_t st) {
+    RQPlan pl;
+    if (rq_plan(M, K, G, &pl) != 0) return hipErrorInvalidValue;
+    if (M == 0) return hipSuccess;
+    dim3 grid(pl.grid), block(pl.block);
+#define RQ_CASE(NP)                                                                              \
+    case NP:                                                                                     \
+        hipLaunchKernelGGL((rotquant_kernel<DT, G, NP, STOCH>), grid, block, 0, st, x, noise, q, s, \
+                           M, K, pl.tpr, pl.rows_per_wg);                                        \
+        break;
+    switch (pl.npass) {
+        RQ_CASE(1) RQ_CASE(2) RQ_CASE(3) RQ_CASE(4) RQ_CASE(5) RQ_CASE(6) RQ_CASE(7) RQ_CASE(8)
+        default: return hipErrorInvalidValue;
+    }
+#undef RQ_CASE
+    return hipGetLastError();
+}
+
+template <int DT, bool STOCH>
+static hipError_t rq_launch_dt(const void* x, const void* noise, int8_t* q, float* s, int M, int K, int G,
+                               hipStream_t st) {
+    switch (G) {
+        case 16: return rq_launch_g<DT, 16, STOCH>(x, noise, q, s, M, K, st);
+        case 64: return rq_launch_g<DT, 64, STOCH>(x, noise, q, s, M, K, st);
+        case 256: return rq_launch_g<DT, 256, STOCH>(x, noise, q, s, M, K, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t rotquant_launch(const void* x, int in_dtype, const void* noise, int8_t* q, float* s,
+                           int M, int K, int G, hipStream_t st) {
+    const bool stoch = noise != nullptr;
+    switch (in_dtype) {
+        case DT_F32: return stoch ? rq_launch_dt<DT_F32, true>(x, noise, q, s, M, K, G, st)
+                                  : rq_launch_dt<DT_F32, false>(x, noise, q, s, M, K, G, st);
+        case DT_BF16: return stoch ? rq_launch_dt<DT_BF16, true>(x, noise, q, s, M, K, G, st)
+                                   : rq_launch_dt<DT_BF16, false>(x, noise, q, s, M, K, G, st);
+        case DT_F16: return stoch ? rq_launch_dt<DT_F16, true>(x, noise, q, s, M, K, G, st)
+                                  : rq_launch_dt<DT_F16, false>(x, noise, q, s, M, K, G, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+int rotquant_max_k() { return 8 * kMaxThreads * kChunk; }
+
+}  // namespace convrot

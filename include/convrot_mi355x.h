@@ -1,0 +1,90 @@
+/*
+ * C-ABI of the gfx950 (MI355X) W4A4 ConvRot linear path.
+ *
+ * Library: comfyui-int4-convrot-rdna4_amd/_int4/libconvrot_gfx950.so
+ *
+ * Conventions (the same as the reference's ctypes boundary, so its bindings
+ * load this library unchanged; reference _int4/hip_loader.py:42-71):
+ *   - all pointers are device pointers; the caller allocates every buffer
+ *     (outputs included); the library holds no device memory;
+ *   - work is enqueued asynchronously on `stream` (a hipStream_t, e.g.
+ *     torch.cuda.current_stream().cuda_stream); nothing synchronises;
+ *   - dtype codes: input 0 = f32, 1 = bf16, 2 = f16; output 0 = f32, 1 = bf16
+ *     (reference _int4/hip_loader.py:38-39);
+ *   - return value: 0 on success, -1 on invalid arguments, otherwise the
+ *     hipError_t of the launch (no device synchronisation).
+ *   - packed int4 layout: int8 [rows, K/2], element 2j in the low nibble of
+ *     byte j, 2j+1 in the high nibble (reference _int4/_codec.py:19-25).
+ */
+#ifndef CONVROT_MI355X_H
+#define CONVROT_MI355X_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * Fused ConvRot rotation + rowwise int4 quantization + nibble packing.
+ *   x        [M, K] in_dtype (row-major, contiguous)
+ *   qout     int8 [M, K/2]  packed codes in [-7, 7]
+ *   scaleout f32 [M]        per-row scale, an exact value of in_dtype
+ * G in {16, 64, 256}, K % G == 0, K <= 32768.
+ * Arithmetic: the reference eager path (_int4/eager.py:65-79, 104-120):
+ * exactly rounded rotation, s = dt(fl32(absmax/7)), q = rint_even(dt(fl32(x/s))).
+ * Replaces: ck_convrot_quant_int4, reference _int4/int4_gemm.hip:650-660
+ * (bound at _int4/hip_loader.py:56-61, called at :74-92).
+ */
+int ck_convrot_quant_int4(const void* x, int in_dtype, void* qout, void* scaleout,
+                          int M, int K, int G, void* stream);
+
+/*
+ * W4A4 GEMM with int32 accumulation and the dequant epilogue:
+ *   out[m, n] = fl32(fl32(fl32(acc * xscale[m]) * wscale[n]) + bias[n])
+ *   acc[m, n] = sum_k qx[m, k] * qw[n, k]
+ * Xp int8 [M, K/2], Wp int8 [N, K/2], xscale f32 [M], wscale f32 [N],
+ * bias f32 [N] or NULL, out [M, N] f32 (out_dtype 0) or bf16 (out_dtype 1,
+ * one RNE of the f32 value).  K % 32 == 0.
+ * Replaces: ck_int4_convrot_gemm, reference _int4/int4_gemm.hip:711-741
+ * (bound at _int4/hip_loader.py:50-52, called at :158-207).
+ */
+int ck_int4_convrot_gemm(const void* Xp, const void* Wp, const void* xscale, const void* wscale,
+                         const void* bias, void* out, int M, int N, int K, int out_dtype,
+                         void* stream);
+
+/*
+ * ck_int4_convrot_gemm with an explicit epilogue:
+ *   epilogue 0: f32 output, as ck_int4_convrot_gemm out_dtype 0
+ *   epilogue 1: bf16 output, as ck_int4_convrot_gemm out_dtype 1
+ *   epilogue 2: bf16 output through the eager bf16 rounding chain
+ *               o1 = bf16(acc), o2 = bf16(o1*bf16(xs)), o3 = bf16(o2*bf16(ws)),
+ *               o4 = bf16(o3 + bf16(bias))  (_int4/eager.py:162-168)
+ *   epilogue 3: int32 accumulators only (out is int32 [M, N]; scales unused)
+ * Extends the same reference export (_int4/int4_gemm.hip:711-741); epilogue 3
+ * is the accumulator dump used to prove the integer stage bit-exact.
+ */
+int cr_int4_convrot_gemm_ex(const void* Xp, const void* Wp, const void* xscale, const void* wscale,
+                            const void* bias, void* out, int M, int N, int K, int epilogue,
+                            void* stream);
+
+/*
+ * ck_convrot_quant_int4 with stochastic rounding: q = clamp(floor(dt(t + u)), -7, 7)
+ * with t = dt(fl32(xr/s)) and u = noise [M, K] (in_dtype, uniform [0, 1)), the
+ * weight-quantization mode of _int4/eager.py:92-109 (the caller draws u with the
+ * same generator call as the reference, _int4/eager.py:92-101).
+ * Replaces the torch stochastic branch of quantize_convrot_w4a4_weight
+ * (_int4/eager.py:123-135), which has no native counterpart in the reference.
+ */
+int cr_convrot_quant_int4_stochastic(const void* x, int in_dtype, const void* noise, void* qout,
+                                     void* scaleout, int M, int K, int G, void* stream);
+
+/* Largest K accepted by the quantization entry points. */
+int cr_max_quant_k(void);
+
+/* ABI version of this library (increments on any signature change). */
+int cr_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CONVROT_MI355X_H */

@@ -1,0 +1,201 @@
+"""CPU-only checks: the C-ABI library loads and exports what the header
+declares, the host-side API validates like the reference, the codec and the
+Linear replacement's load-time dispatch logic (with a fake comfy package)."""
+import ctypes
+import os
+import re
+import sys
+import types
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import ROOT, import_pkg
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "convrot_mi355x.h")).read()
+    return re.findall(r"^\s*int\s+(\w+)\s*\(", text, flags=re.M)
+
+
+def test_header_declares_reference_entry_points():
+    syms = header_symbols()
+    # names a binding of the reference's ctypes loader resolves (hip_loader.py:50-61)
+    assert "ck_convrot_quant_int4" in syms
+    assert "ck_int4_convrot_gemm" in syms
+
+
+def test_library_exports_every_declared_symbol(native):
+    lib = native.load_library()
+    for name in header_symbols():
+        assert hasattr(lib, name), name
+    raw = ctypes.CDLL(native.lib_path())
+    for name in header_symbols():
+        getattr(raw, name)
+    assert set(native.exported_symbols()) == set(header_symbols())
+
+
+def test_library_queries_without_gpu(native):
+    lib = native.load_library()
+    assert lib.cr_abi_version() == 1
+    assert lib.cr_max_quant_k() == 32768
+
+
+def test_argument_errors_return_minus_one(native):
+    """Invalid arguments are rejected before any device work (-1)."""
+    lib = native.load_library()
+    n = ctypes.c_void_p(0)
+    assert lib.ck_convrot_quant_int4(n, 1, n, n, 4, 256, 32, n) == -1      # bad G
+    assert lib.ck_convrot_quant_int4(n, 1, n, n, 4, 100, 16, n) == -1      # K % G
+    assert lib.ck_convrot_quant_int4(n, 7, n, n, 4, 256, 256, n) == -1     # bad dtype
+    assert lib.ck_convrot_quant_int4(n, 1, n, n, 4, 65536, 256, n) == -1   # K too large
+    assert lib.ck_int4_convrot_gemm(n, n, n, n, n, n, 4, 4, 48, 1, n) == -1  # K % 32
+    assert lib.ck_int4_convrot_gemm(n, n, n, n, n, n, 4, 4, 64, 5, n) == -1  # out dtype
+    assert lib.cr_int4_convrot_gemm_ex(n, n, n, n, n, n, 4, 4, 64, 9, n) == -1
+    assert lib.cr_convrot_quant_int4_stochastic(n, 1, n, n, n, 4, 256, 256, n) == -1  # no noise
+
+
+def test_pick_groupsize(backend):
+    assert backend.pick_groupsize(3072) == 256
+    assert backend.pick_groupsize(12288) == 256
+    assert backend.pick_groupsize(3840) == 256
+    assert backend.pick_groupsize(192) == 64
+    assert backend.pick_groupsize(80) == 16
+    assert backend.pick_groupsize(40) is None
+
+
+def test_linear_validation_errors(backend):
+    x = torch.zeros(4, 512, dtype=torch.bfloat16)
+    qw = torch.zeros(8, 256, dtype=torch.int8)
+    ws = torch.ones(8)
+    with pytest.raises(ValueError):
+        backend.convrot_w4a4_linear(x, qw, ws, linear_dtype="fp8")
+    with pytest.raises(ValueError):
+        backend.convrot_w4a4_linear(x, qw, ws, quant_group_size=32)
+    with pytest.raises(ValueError):
+        backend.convrot_w4a4_linear(x, torch.zeros(8, 128, dtype=torch.int8), ws)
+    with pytest.raises(ValueError):
+        backend.convrot_w4a4_linear(torch.zeros(4, 80, dtype=torch.bfloat16),
+                                    torch.zeros(8, 40, dtype=torch.int8), ws, convrot_groupsize=256)
+
+
+def test_weight_validation_errors(backend):
+    with pytest.raises(ValueError):
+        backend.quantize_convrot_w4a4_weight(torch.zeros(8, 512), quant_group_size=32)
+    with pytest.raises(ValueError):
+        backend.quantize_convrot_w4a4_weight(torch.zeros(8, 80), convrot_groupsize=16)  # K % 64
+    with pytest.raises(ValueError):
+        backend.quantize_convrot_w4a4_weight(torch.zeros(8, 8, 8))
+
+
+def test_codec_torch_roundtrip(backend, oracle):
+    from importlib import import_module
+    codec = import_module("comfyui-int4-convrot-rdna4_amd._int4._codec")
+    allb = torch.arange(-128, 128, dtype=torch.int32).to(torch.int8).reshape(2, 128)
+    codes = codec._unpack_int4_row_major(allb)
+    assert np.array_equal(codes.numpy(), oracle.unpack(allb.numpy()))
+    assert torch.equal(codec._pack_int4_row_major(codes), allb)
+    assert codec._INT4_GROUP_SIZE == 64 and codec._INT4_MAX == 7
+
+
+def test_dequantize_matches_oracle(backend, oracle, goldens):
+    q = torch.from_numpy(goldens["w64_q"])
+    s = torch.from_numpy(goldens["w64_s"])
+    deq = backend.dequantize_convrot_w4a4_weight(q, s, convrot_groupsize=64)
+    np.testing.assert_allclose(deq.numpy(), goldens["w64_deq"], rtol=0, atol=2e-6)
+
+
+# ----------------------------------------------------------------------------
+# Int4ConvRotOps load-time logic with a fake comfy package
+# ----------------------------------------------------------------------------
+
+def install_fake_comfy():
+    if "comfy.ops" in sys.modules and getattr(sys.modules["comfy.ops"], "_FAKE", False):
+        return
+    comfy = types.ModuleType("comfy")
+    ops = types.ModuleType("comfy.ops")
+    ops._FAKE = True
+
+    class manual_cast:
+        class Linear(torch.nn.Linear):
+            comfy_cast_weights = True
+
+            def reset_parameters(self):
+                return None
+
+            def forward(self, x):
+                w = self.weight.to(x.device, x.dtype)
+                b = self.bias.to(x.device, x.dtype) if self.bias is not None else None
+                return torch.nn.functional.linear(x, w, b)
+
+    ops.manual_cast = manual_cast
+    comfy.ops = ops
+    sys.modules["comfy"] = comfy
+    sys.modules["comfy.ops"] = ops
+
+
+@pytest.fixture(scope="module")
+def ops_mod():
+    install_fake_comfy()
+    from importlib import import_module, reload
+    import_pkg()
+    m = import_module("comfyui-int4-convrot-rdna4_amd.int4_ops")
+    if m.Int4ConvRotOps is None:
+        m = reload(m)
+    assert m.Int4ConvRotOps is not None
+    return m
+
+
+def test_ops_should_quantize_and_mode(ops_mod):
+    Ops = ops_mod.Int4ConvRotOps
+    Ops.excluded_names = ["img_in"]
+    Ops.excluded_exact = {"double_blocks.0.img_attn.proj"}
+    Ops.int8_exact = {"double_blocks.0.img_mlp.0"}
+    try:
+        lin = Ops.Linear(3072, 64, bias=True)
+        w = torch.zeros(64, 3072)
+        assert lin._should_quantize("diffusion_model.double_blocks.0.img_attn.qkv.", w)
+        assert not lin._should_quantize("diffusion_model.img_in.", w)
+        assert not lin._should_quantize("diffusion_model.double_blocks.0.img_attn.proj.", w)
+        assert lin._quant_mode("model.diffusion_model.double_blocks.0.img_mlp.0.") == "int8"
+        assert lin._quant_mode("double_blocks.0.img_mlp.2.") == "int4"
+        small = Ops.Linear(256, 64)
+        assert not small._should_quantize("x.", torch.zeros(64, 256))      # < min_in_features
+        odd = Ops.Linear(520, 64)
+        assert not odd._should_quantize("x.", torch.zeros(64, 520))        # no groupsize
+        assert not lin._should_quantize("x.", torch.zeros(3072))           # not 2-D
+    finally:
+        Ops.excluded_names, Ops.excluded_exact, Ops.int8_exact = [], set(), set()
+
+
+def test_ops_key_normalization(ops_mod):
+    L = ops_mod.Int4ConvRotOps.Linear
+    assert L._normalize_lora_key("diffusion_model.a.b.weight") == "a.b.weight"
+    assert L._normalize_lora_key("transformer.x") == "x"
+    assert L._exact_key("model.diffusion_model.blk.0.") == "blk.0"
+    assert L._normalize_lora_key(3) == 3
+
+
+def test_ops_quant_tag_parsing(ops_mod):
+    tag = lambda d: torch.tensor(list(__import__("json").dumps(d).encode()), dtype=torch.uint8)
+    assert ops_mod._parse_quant_tag(tag({"format": "convrot_w4a4", "convrot_groupsize": 64})) == (True, 64)
+    assert ops_mod._parse_quant_tag(tag({"format": "float8_e4m3fn"})) == (False, None)
+    assert ops_mod._parse_quant_tag(tag({"format": "int8_tensorwise"})) == (False, None)
+    assert ops_mod._parse_quant_tag(tag({"format": "int8_tensorwise", "convrot": True})) == (True, None)
+
+
+def test_ops_plain_layer_loads_bf16(ops_mod):
+    """A layer that is not quantized (too narrow) takes the plain load path."""
+    lin = ops_mod.Int4ConvRotOps.Linear(256, 32, bias=True)
+    sd = {"weight": torch.randn(32, 256), "bias": torch.randn(32)}
+    lin.load_state_dict(sd)
+    assert lin._q is None and lin._qmode is None
+    x = torch.randn(3, 256)
+    torch.testing.assert_close(lin(x), x @ sd["weight"].T + sd["bias"])
+
+
+def test_ops_refuses_unknown_prequant_layout(ops_mod):
+    lin = ops_mod.Int4ConvRotOps.Linear(3072, 32, bias=False)
+    sd = {"weight": torch.zeros(32, 100, dtype=torch.int8), "weight_scale": torch.ones(32)}
+    assert lin._load_prequantized(dict(sd), "", "weight", "weight_scale", sd["weight"]) is False
