@@ -1,0 +1,250 @@
+"""Benchmark of the gfx950 W4A4 ConvRot linear path.
+
+One step = the four quantized linears of a Flux-class DiT block at M = 4608
+tokens (4096 image + 512 text at 1024^2), each run as on the forward path:
+fused rotate+int4-quantize of the bf16 activation, then the W4A4 GEMM with the
+dequant + bias epilogue to bf16.
+
+    qkv      3072 -> 9216      proj     3072 -> 3072
+    mlp_up   3072 -> 12288     mlp_down 12288 -> 3072
+
+Inputs are synthetic and resident in HBM before timing: x ~ N(0,1) with 1% of
+channels x20, W ~ N(0, 0.02) in fp16 quantized once by the same kernel (load
+time, untimed), bias ~ N(0, 0.01).  Every linear has its own activation buffer
+(~450 MB live per step, beyond the 256 MB Infinity Cache).
+
+Prints one JSON line: value = effective W4A4 linear TOPS of the whole step
+(2*M*N*K summed over the four linears / step time, rotate+quant included).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import importlib
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+
+METRIC = "W4A4 linear TOPS (%int8 MFMA peak) + rotate-quant GB/s at M=4608,K=3072"
+PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
+M_TOKENS = 4608
+G = 256
+LINEARS = [("qkv", 3072, 9216), ("proj", 3072, 3072), ("mlp_up", 3072, 12288), ("mlp_down", 12288, 3072)]
+
+
+def rq_bytes(M, K):
+    """Algorithmic HBM bytes of one rotate+quant launch: read bf16, write nibbles + scales."""
+    return M * K * 2 + M * K // 2 + 4 * M
+
+
+class Linear:
+    def __init__(self, torch, native, name, K, N, seed):
+        from inputs import normal_bias, normal_weight, outlier_activations
+        dev = torch.device("cuda")
+        self.name, self.K, self.N, self.M = name, K, N, M_TOKENS
+        self.x = outlier_activations(M_TOKENS, K, seed=seed).to(dev)
+        w = normal_weight(N, K, seed=seed + 1).to(dev)
+        self.qw, self.ws = native.convrot_quant_int4(w, G)         # load-time weight quantization
+        self.bias = normal_bias(N, seed=seed + 2).to(dev).float()
+        self.qx = torch.empty((M_TOKENS, K // 2), dtype=torch.int8, device=dev)
+        self.xs = torch.empty((M_TOKENS,), dtype=torch.float32, device=dev)
+        self.out = torch.empty((M_TOKENS, N), dtype=torch.bfloat16, device=dev)
+        del w
+
+    def ops(self):
+        return 2.0 * self.M * self.N * self.K
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="approximate CPU time for the oracle baseline (0 disables it)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 1 GiB device copy (counter calibration)")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (every box here has one); --gpus {args.gpus} "
+              "is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    importlib.import_module("comfyui-int4-convrot-rdna4_amd")
+    native = importlib.import_module("comfyui-int4-convrot-rdna4_amd._int4.native")
+    if not native.is_available():
+        raise SystemExit("libconvrot_gfx950.so is not loadable on a gfx950 device; nothing to measure")
+    lib = native.load_library()
+    stream = torch.cuda.current_stream()
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+
+    lins = [Linear(torch, native, n, K, N, seed=10 * i) for i, (n, K, N) in enumerate(LINEARS)]
+    torch.cuda.synchronize()
+
+    vp = ctypes.c_void_p
+    calls = []   # (kind, index, fn, args)
+    for i, L in enumerate(lins):
+        calls.append(("rq", i, lib.ck_convrot_quant_int4,
+                      (vp(L.x.data_ptr()), 1, vp(L.qx.data_ptr()), vp(L.xs.data_ptr()), L.M, L.K, G, sptr)))
+        calls.append(("gemm", i, lib.ck_int4_convrot_gemm,
+                      (vp(L.qx.data_ptr()), vp(L.qw.data_ptr()), vp(L.xs.data_ptr()), vp(L.ws.data_ptr()),
+                       vp(L.bias.data_ptr()), vp(L.out.data_ptr()), L.M, L.N, L.K, 1, sptr)))
+
+    def step(events=None):
+        for j, (_, _, fn, a) in enumerate(calls):
+            if events is not None:
+                events[j][0].record(stream)
+            rc = fn(*a)
+            if events is not None:
+                events[j][1].record(stream)
+            if rc != 0:
+                raise RuntimeError(f"launch failed rc={rc}")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # timed region: K steps, bracketed by synchronize on both sides
+    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
+           for _ in calls] for _ in range(args.steps)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    t_start.record(stream)
+    for s in range(args.steps):
+        step(ev[s])
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = t_start.elapsed_time(t_end) / args.steps
+
+    # per-launch durations (HIP events on the launch stream)
+    dur = {}
+    for s in range(args.steps):
+        for j, (kind, i, _, _) in enumerate(calls):
+            dur.setdefault((kind, i), []).append(ev[s][j][0].elapsed_time(ev[s][j][1]) * 1e-3)  # seconds
+    avg = {k: sum(v) / len(v) for k, v in dur.items()}
+
+    total_ops = sum(L.ops() for L in lins)
+    value = total_ops / (ms_step * 1e-3) / 1e12
+    gemm_time = sum(avg[("gemm", i)] for i in range(len(lins)))
+    gemm_launch_avg = gemm_time / len(lins)
+    gemm_ops_avg = total_ops / len(lins)
+    gemm_tops = gemm_ops_avg / gemm_launch_avg / 1e12
+    rq_time = sum(avg[("rq", i)] for i in range(len(lins)))
+    rq_b = sum(rq_bytes(L.M, L.K) for L in lins)
+    rq_gbs = rq_b / rq_time / 1e9
+    metric_rq = avg[("rq", 1)]                   # proj input: M=4608, K=3072
+    metric_rq_gbs = rq_bytes(M_TOKENS, 3072) / metric_rq / 1e9
+
+    detail = {}
+    for i, L in enumerate(lins):
+        detail[L.name] = {
+            "K": L.K, "N": L.N,
+            "rotate_quant_us": round(avg[("rq", i)] * 1e6, 2),
+            "rotate_quant_GBps": round(rq_bytes(L.M, L.K) / avg[("rq", i)] / 1e9, 1),
+            "gemm_us": round(avg[("gemm", i)] * 1e6, 2),
+            "gemm_TOPS": round(L.ops() / avg[("gemm", i)] / 1e12, 1),
+        }
+
+    copy_cal = None
+    if args.copy_calibration:
+        a = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        copy_cal = {"bytes_read": 1 << 30, "bytes_written": 1 << 30}
+        del a, b
+
+    cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": "Flux-class DiT block W4A4 ConvRot linears (qkv 3072->9216, proj 3072->3072, "
+                        "mlp_up 3072->12288, mlp_down 12288->3072), M=4608 tokens, bf16 in/out, G=256",
+            "M": M_TOKENS, "convrot_groupsize": G, "linears": [[n, K, N] for n, K, N in LINEARS],
+        },
+        "roofline": {
+            "kernel": "w4a4_gemm_kernel<EPI_BF16>",
+            "bound": "mfma",
+            "achieved": round(gemm_tops, 1),
+            "peak": PEAK_INT8_TOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
+            "traffic": None,
+        },
+        "rotate_quant": {
+            "kernel": "rotquant_kernel<bf16,256>",
+            "bound": "hbm",
+            "GBps_at_M4608_K3072": round(metric_rq_gbs, 1),
+            "frac_at_M4608_K3072": round(metric_rq_gbs / PEAK_HBM_GBS, 4),
+            "GBps_all_launches": round(rq_gbs, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+        },
+        "gemm_TOPS": round(gemm_tops, 1),
+        "gemm_pct_int8_peak": round(100 * gemm_tops / PEAK_INT8_TOPS, 2),
+        "detail": detail,
+        "cpu_baseline": cpu,
+        "host_wall_s": round(wall, 3),
+    }
+    if copy_cal:
+        line["copy_calibration"] = copy_cal
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(target_s: float):
+    """The oracle (plain C, one thread) on a bounded sample of the same step:
+    rows of the proj linear (3072 -> 3072) through rotate+quant, exact integer
+    GEMM and the fp32 epilogue.  Reported in the same unit (effective TOPS)."""
+    import numpy as np
+    import torch
+    import oracle
+    from inputs import bf16_bits, normal_weight, outlier_activations
+
+    K, N = 3072, 3072
+    w = normal_weight(N, K, seed=11).view(torch.int16).numpy().view(np.uint16)
+    qw, ws = oracle.quantize_weight(w, oracle.F16, G)
+    bias = np.zeros(N, dtype=np.float32)
+
+    def run(rows):
+        x = bf16_bits(outlier_activations(rows, K, seed=rows))
+        t0 = time.perf_counter()
+        q, xs, _ = oracle.rotquant(x, oracle.BF16, G)
+        acc = oracle.int_gemm(q, qw)
+        oracle.epilogue_f32(acc, xs, ws, bias, out_bf16=True)
+        return time.perf_counter() - t0
+
+    t = run(8)
+    rows = int(max(8, min(M_TOKENS, 8 * target_s / max(t, 1e-6))))
+    t = run(rows)
+    ops = 2.0 * rows * N * K
+    return {"value": round(ops / t / 1e12, 6), "unit": "TOPS", "cores": 1, "kind": "port",
+            "sample": f"oracle (C, 1 thread): {rows} of the 4608 rows of the proj linear 3072->3072 "
+                      f"(rotate+quant, int GEMM, epilogue), {t:.1f} s",
+            "seconds": round(t, 2)}
+
+
+if __name__ == "__main__":
+    main()
