@@ -47,10 +47,12 @@ constexpr int kPad = 17;         // fp64 words per lane slot in the transpose bu
 
 // radix-4 stage of the regular Hadamard H4 on four values:
 // H4 v = (sum v) 1 - 2 reverse(v)   (H4 as in _int4/eager.py:32-36)
+// (every value is exact: sums of inputs times powers of two; fma keeps one op)
 __device__ __forceinline__ void h4_stage(double& a, double& b, double& c, double& d, double scale) {
-    double S = ((a + b) + (c + d)) * scale;
-    double t = 2.0 * scale;
-    double na = S - t * d, nb = S - t * c, nc = S - t * b, nd = S - t * a;
+    const double S = (scale == 1.0) ? ((a + b) + (c + d)) : ((a + b) + (c + d)) * scale;
+    const double t = -2.0 * scale;
+    const double na = __builtin_fma(t, d, S), nb = __builtin_fma(t, c, S);
+    const double nc = __builtin_fma(t, b, S), nd = __builtin_fma(t, a, S);
     a = na; b = nb; c = nc; d = nd;
 }
 
@@ -256,6 +258,289 @@ __global__ __launch_bounds__(kMaxThreads) void rotquant_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Wave-per-row kernel (no workgroup barriers).
+//
+// Each 64-lane wave owns whole rows and walks them persistently
+// (row = global wave id, += number of waves).  A row of K elements is
+// K/16 chunks handled in np = ceil(K/1024) passes of 64 lanes; the chunk of
+// the next pass (or of the next row's first pass) is loaded while the current
+// one is computed.  The fp64 transpose and the code gather use a private LDS
+// region per wave, so lanes only synchronise with their own wave, and the row
+// absmax is a shuffle reduction.  Rounded rotated values stay in registers as
+// packed 16-bit pairs until the row scale is known.
+// ---------------------------------------------------------------------------
+
+constexpr int kWaves = 4;      // independent waves per workgroup
+
+template <int DT>
+struct ChunkRegs { uint4 r[DT == DT_F32 ? 4 : 2]; };
+
+template <int DT>
+__device__ __forceinline__ void load_regs(const void* __restrict__ x, size_t elem, ChunkRegs<DT>& c) {
+    constexpr int esz = DT == DT_F32 ? 4 : 2;
+    const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(x) + elem * esz);
+#pragma unroll
+    for (int q = 0; q < (DT == DT_F32 ? 4 : 2); ++q) c.r[q] = p[q];
+}
+
+template <int DT>
+__device__ __forceinline__ void regs_to_f64(const ChunkRegs<DT>& c, double (&v)[16]) {
+    if constexpr (DT == DT_F32) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            v[4 * q + 0] = (double)__uint_as_float(c.r[q].x);
+            v[4 * q + 1] = (double)__uint_as_float(c.r[q].y);
+            v[4 * q + 2] = (double)__uint_as_float(c.r[q].z);
+            v[4 * q + 3] = (double)__uint_as_float(c.r[q].w);
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint32_t w[4] = {c.r[q].x, c.r[q].y, c.r[q].z, c.r[q].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if constexpr (DT == DT_BF16) {
+                    v[8 * q + 2 * j] = (double)bf16lo_to_f32(w[j]);
+                    v[8 * q + 2 * j + 1] = (double)bf16hi_to_f32(w[j]);
+                } else {
+                    v[8 * q + 2 * j] = (double)f16bits_to_f32(w[j]);
+                    v[8 * q + 2 * j + 1] = (double)f16bits_to_f32(w[j] >> 16);
+                }
+            }
+        }
+    }
+}
+
+// storage of 16 rounded values: packed 16-bit pairs for bf16/f16, floats for f32
+template <int DT> struct Held { uint32_t w[8]; };
+template <> struct Held<DT_F32> { float f[16]; };
+
+template <int DT>
+__device__ __forceinline__ void hold(Held<DT>& h, int i, float a, float b) {   // values i, i+1
+    if constexpr (DT == DT_F32) {
+        h.f[i] = a; h.f[i + 1] = b;
+    } else if constexpr (DT == DT_BF16) {
+        h.w[i >> 1] = (__float_as_uint(a) >> 16) | (__float_as_uint(b) & 0xffff0000u);
+    } else {
+        h.w[i >> 1] = (uint32_t)__half_as_ushort(__float2half_rn(a)) |
+                      ((uint32_t)__half_as_ushort(__float2half_rn(b)) << 16);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ float held(const Held<DT>& h, int i) {
+    if constexpr (DT == DT_F32) return h.f[i];
+    else if constexpr (DT == DT_BF16) return (i & 1) ? bf16hi_to_f32(h.w[i >> 1]) : bf16lo_to_f32(h.w[i >> 1]);
+    else return f16bits_to_f32((i & 1) ? (h.w[i >> 1] >> 16) : h.w[i >> 1]);
+}
+
+__device__ __forceinline__ void wave_sync() {
+    // all lanes of a wave issue LDS operations in program order; keep the
+    // compiler from moving LDS accesses across this point
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// fp64 -> float with the bits below float precision folded into a sticky bit
+// (see round_f64_to_dt): rounding the result once to bf16/f16 equals rounding
+// the fp64 value once.  Monotone, so the max of jammed values rounds to the
+// max of the rounded values.
+// The sticky bit goes to fp64 mantissa bit 29, the last bit a float keeps,
+// so the conversion is exact; mantissa bits 31..29 of the input are below the
+// bf16 / f16 guard bit and only their "any set" matters.
+__device__ __forceinline__ float jam_to_f32(double d) {
+    const uint64_t u = (uint64_t)__double_as_longlong(d);
+    const uint32_t lo = min((uint32_t)u, 1u) << 29;
+    return (float)__longlong_as_double((long long)((u & 0xffffffff00000000ull) | lo));
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {   // both RNE in one v_cvt_pk_bf16_f32
+    const bf16x2_t h = __builtin_convertvector((f32x2_t){a, b}, bf16x2_t);
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+template <int DT, int G, int NPMAX>
+__global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
+        const void* __restrict__ x, int8_t* __restrict__ qout, float* __restrict__ sout, int M, int K) {
+    constexpr int LPG = G / kChunk;
+    __shared__ double tbuf_all[kWaves][64 * kPad];
+    __shared__ uint32_t cbuf_all[kWaves][64 * 4];
+
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    double* tbuf = tbuf_all[wv];
+    uint8_t* cb = reinterpret_cast<uint8_t*>(cbuf_all[wv]);
+    const int nwaves = gridDim.x * kWaves;
+    const int nchunks = K / kChunk;
+    const int np = (nchunks + 63) >> 6;
+    const int gl = lane % LPG;
+    const int gfirst = lane - gl;
+    const float kMagic = 12582912.0f;
+
+    ChunkRegs<DT> nxt;
+    int row = blockIdx.x * kWaves + wv;
+    if (row < M && lane < nchunks) load_regs<DT>(x, (size_t)row * K + (size_t)lane * kChunk, nxt);
+
+    for (; row < M; row += nwaves) {
+        Held<DT> hv[NPMAX];
+        float lmax = 0.0f;
+#pragma unroll
+        for (int p = 0; p < NPMAX; ++p) {
+            if (p < np) {
+                ChunkRegs<DT> cur = nxt;
+                {   // prefetch: next pass of this row, or the first pass of the next row
+                    const int nr = (p + 1 < np) ? row : row + nwaves;
+                    const int nc = (p + 1 < np) ? (p + 1) * 64 + lane : lane;
+                    if (nr < M && nc < nchunks) load_regs<DT>(x, (size_t)nr * K + (size_t)nc * kChunk, nxt);
+                }
+                const int c = p * 64 + lane;
+                const bool ok = c < nchunks;
+                double v[16];
+                if (nchunks & 63) {             // ragged last pass (wave-uniform branch)
+                    if (!ok) cur = ChunkRegs<DT>{};
+                }
+                regs_to_f64<DT>(cur, v);
+                if constexpr (G == 16) {
+                    stage16<1>(v, 1.0);
+                    stage16<4>(v, 0.25);
+                } else {
+                    stage16<1>(v, 1.0);
+                    stage16<4>(v, 1.0);
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) tbuf[lane * kPad + i] = v[i];
+                    wave_sync();
+                    if constexpr (G == 256) {
+#pragma unroll
+                        for (int m = 0; m < 16; ++m) v[m] = tbuf[(gfirst + m) * kPad + gl];
+                        stage16<1>(v, 1.0);
+                        stage16<4>(v, 1.0 / 16.0);
+                    } else {
+#pragma unroll
+                        for (int b = 0; b < 4; ++b)
+#pragma unroll
+                            for (int a = 0; a < 4; ++a) v[a + 4 * b] = tbuf[(gfirst + b) * kPad + 4 * gl + a];
+                        stage16<4>(v, 1.0 / 8.0);
+                    }
+                    wave_sync();
+                }
+#pragma unroll
+                for (int i = 0; i < 16; i += 2) {
+                    if constexpr (DT == DT_BF16) {
+                        const float f0 = jam_to_f32(v[i]), f1 = jam_to_f32(v[i + 1]);
+                        hv[p].w[i >> 1] = pack_bf16x2(f0, f1);
+                        lmax = fmaxf(lmax, fmaxf(fabsf(f0), fabsf(f1)));
+                    } else {
+                        const float r0 = round_f64_to_dt<DT>(v[i]);
+                        const float r1 = round_f64_to_dt<DT>(v[i + 1]);
+                        hold<DT>(hv[p], i, r0, r1);
+                        lmax = fmaxf(lmax, fmaxf(fabsf(r0), fabsf(r1)));
+                    }
+                }
+            }
+        }
+        // row absmax across the wave (invalid chunks hold zeros)
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, off));
+        // bf16: lmax is a jammed value; its RNE is the max of the rounded values
+        const float a = fmaxf(round_to_dt<DT>(lmax), clamp_floor<DT>());
+        const float s = round_to_dt<DT>(a / 7.0f);
+        if (lane == 0) sout[row] = s;
+        const float rinv32 = 1.0f / s;
+        const double rinv = 1.0 / (double)s;
+
+#pragma unroll
+        for (int p = 0; p < NPMAX; ++p) {
+            if (p < np) {
+                const int c = p * 64 + lane;
+                const bool ok = c < nchunks;
+#pragma unroll
+                for (int i = 0; i < 16; i += 2) {
+                    float z0, z1;
+                    if constexpr (DT == DT_BF16) {
+                        // one packed RNE for both quotients; |z| <= 7.03 because
+                        // s >= bf16(absmax)/7 rounded, so rint stays in [-7, 7]
+                        const uint32_t zz = pack_bf16x2(bf16lo_to_f32(hv[p].w[i >> 1]) * rinv32,
+                                                        bf16hi_to_f32(hv[p].w[i >> 1]) * rinv32);
+                        z0 = bf16lo_to_f32(zz);
+                        z1 = bf16hi_to_f32(zz);
+                    } else {
+                        float zz[2];
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const float xv = held<DT>(hv[p], i + h);
+                            float z;
+                            if constexpr (DT == DT_F32) z = xv / s;
+                            else z = round_to_dt<DT>((float)((double)xv * rinv));
+                            if constexpr (DT == DT_F16) z = (z == z) ? z : 0.0f;
+                            zz[h] = fminf(fmaxf(z, -7.0f), 7.0f);
+                        }
+                        z0 = zz[0];
+                        z1 = zz[1];
+                    }
+                    // low byte of the float bits of z + 1.5*2^23 is rint_even(z) (two's complement)
+                    const int e0 = final_elem<G>(gl, i), e1 = final_elem<G>(gl, i + 1);
+                    cb[(gfirst + e0 / kChunk) * 16 + (e0 % kChunk)] = (uint8_t)__float_as_uint(z0 + kMagic);
+                    cb[(gfirst + e1 / kChunk) * 16 + (e1 % kChunk)] = (uint8_t)__float_as_uint(z1 + kMagic);
+                }
+                wave_sync();
+                const uint4 w = reinterpret_cast<const uint4*>(cb)[lane];
+                wave_sync();
+                if (ok) {
+                    const uint32_t ws[4] = {w.x & 0x0f0f0f0fu, w.y & 0x0f0f0f0fu, w.z & 0x0f0f0f0fu,
+                                            w.w & 0x0f0f0f0fu};
+                    uint32_t o[2];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const uint32_t t0 = ws[2 * h] | (ws[2 * h] >> 4);
+                        const uint32_t t1 = ws[2 * h + 1] | (ws[2 * h + 1] >> 4);
+                        o[h] = (t0 & 0xffu) | ((t0 >> 8) & 0xff00u) | ((t1 & 0xffu) << 16) | ((t1 << 8) & 0xff000000u);
+                    }
+                    *reinterpret_cast<uint2*>(qout + (size_t)row * (K / 2) + (size_t)c * (kChunk / 2)) =
+                        make_uint2(o[0], o[1]);
+                }
+            }
+        }
+    }
+}
+
+static int g_num_cus = 0;
+
+static int num_cus() {
+    if (g_num_cus == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            g_num_cus = n;
+        else
+            g_num_cus = 256;
+    }
+    return g_num_cus;
+}
+
+template <int DT, int G>
+static hipError_t rq_wave_launch(const void* x, int8_t* q, float* s, int M, int K, hipStream_t st) {
+    const int np = (K / kChunk + 63) / 64;
+    // enough waves to keep every CU busy; each wave then walks rows persistently
+    const int max_wg = num_cus() * 8;
+    int grid = (M + kWaves - 1) / kWaves;
+    if (grid > max_wg) grid = max_wg;
+    dim3 g(grid), b(64 * kWaves);
+    if (np <= 3)
+        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 3>), g, b, 0, st, x, q, s, M, K);
+    else if (np <= 6)
+        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 6>), g, b, 0, st, x, q, s, M, K);
+    else
+        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 12>), g, b, 0, st, x, q, s, M, K);
+    return hipGetLastError();
+}
+
+constexpr int kWaveMaxK = 12 * 64 * kChunk;   // 12288
+
+// ---------------------------------------------------------------------------
 // host-side launch
 // ---------------------------------------------------------------------------
 
@@ -281,9 +566,10 @@ static inline int rq_plan(int M, int K, int G, RQPlan* pl) {
 template <int DT, int G, bool STOCH>
 static hipError_t rq_launch_g(const void* x, const void* noise, int8_t* q, float* s, int M, int K,
                               hipStream_t st) {
+    if (M == 0) return hipSuccess;
+    if (!STOCH && K <= kWaveMaxK) return rq_wave_launch<DT, G>(x, q, s, M, K, st);
     RQPlan pl;
     if (rq_plan(M, K, G, &pl) != 0) return hipErrorInvalidValue;
-    if (M == 0) return hipSuccess;
     dim3 grid(pl.grid), block(pl.block);
 #define RQ_CASE(NP)                                                                              \
     case NP:                                                                                     \

@@ -106,3 +106,15 @@ def test_full_size_sampled_rows(native, oracle, gpu):
     codes = torch.stack([(q.to(torch.int32) << 28) >> 28, (q.to(torch.int32) << 24) >> 28], -1)
     assert int(codes.abs().max()) == 7
     assert bool((codes.abs().amax(dim=(1, 2)) == 7).all())
+
+
+@pytest.mark.parametrize("M,K", [(20000, 3072), (9000, 5120), (16500, 256)])
+def test_persistent_rows_sampled(native, oracle, gpu, M, K):
+    """More rows than resident waves: every wave walks several rows."""
+    x = outlier_activations(M, K, seed=M + K)
+    q, s = native.convrot_quant_int4(x.cuda(), 256)
+    torch.cuda.synchronize()
+    rows = np.concatenate([np.random.RandomState(2).choice(M, 40, replace=False), [0, 1, M - 2, M - 1]])
+    eq, es, _ = oracle.rotquant(host_bits(x[rows]), 1, 256)
+    assert np.array_equal(q.cpu().numpy()[rows], eq)
+    assert np.array_equal(s.cpu().numpy()[rows], es)
