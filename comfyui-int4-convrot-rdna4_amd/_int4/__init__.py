@@ -34,7 +34,12 @@ __all__ = [
     "convrot_w8a8_linear",
     "is_available",
     "pick_groupsize",
+    "fuse_lora_pairs",
+    "MAX_LORA_RANK",
 ]
+
+# largest concatenated rank of the fused LoRA side path (padded to a multiple of 32)
+MAX_LORA_RANK = 128
 
 # dtypes the GEMM emits natively; others compute in fp32 then cast
 # (reference _int4/__init__.py:45)
@@ -153,9 +158,16 @@ def convrot_w4a4_linear(
     convrot_groupsize: int = 256,
     quant_group_size: int = _INT4_GROUP_SIZE,
     linear_dtype: str = "int4",
+    *,
+    lora: tuple[torch.Tensor, torch.Tensor] | None = None,
 ) -> torch.Tensor:
     """Compute ``x @ W.T + bias`` with the gfx950 W4A4 ConvRot path
     (reference _int4/__init__.py:94-138).
+
+    ``lora=(D, U)`` (from :func:`fuse_lora_pairs`) adds the dynamic-LoRA term
+    ``(x @ D.T) @ U.T`` inside the GEMM epilogue (one extra kernel for the
+    down projection), the fused form of the per-adapter side path of the
+    reference's Linear (int4_ops.py:181-192).
 
     Two kernels per call, both on torch's current stream: the fused
     rotate+quantize of x, then the W4A4 GEMM with the dequant epilogue.  Every
@@ -180,10 +192,59 @@ def convrot_w4a4_linear(
         x2d = x2d.to(torch.float32)
     qact, x_scale = native.convrot_quant_int4(x2d, convrot_groupsize)
     out_dtype = x.dtype if x.dtype in _NATIVE_OUT else torch.float32
-    out = native.int4_convrot_gemm(qact, qweight, x_scale, wscales, bias, out_dtype)
+    if lora is None:
+        out = native.int4_convrot_gemm(qact, qweight, x_scale, wscales, bias, out_dtype)
+    else:
+        down, up = lora
+        if down.shape[1] != x2d.shape[1] or up.shape[0] != qweight.shape[0] or up.shape[1] != down.shape[0]:
+            raise ValueError(f"LoRA shapes D {tuple(down.shape)} U {tuple(up.shape)} do not fit "
+                             f"K={x2d.shape[1]} N={qweight.shape[0]}")
+        xd = x2d if x2d.dtype in (torch.bfloat16, torch.float16) else x2d.to(torch.bfloat16)
+        t = native.lora_down(xd, down)
+        epi = native.EPI_BF16 if out_dtype == torch.bfloat16 else native.EPI_F32
+        out = native.int4_convrot_gemm_lora(qact, qweight, x_scale, wscales, bias, t, up, 1.0, epi)
     if out.dtype != x.dtype:
         out = out.to(x.dtype)
     return out.reshape(*orig_shape[:-1], qweight.shape[0])
+
+
+def fuse_lora_pairs(pairs, device=None):
+    """Concatenate plain LoRA adapters into the one (D, U) pair of the fused
+    side path.
+
+    ``pairs``: (down [r, K], up [N, r], scale) per adapter, where scale is the
+    factor the adapter's bypass applies to up(down(x)), i.e. multiplier *
+    alpha / r (reference int4_ops.py:181-192, "h() returns up(down(x)) already
+    scaled by (alpha/rank)*strength").  The scale is folded into U (in fp32,
+    then rounded once to bf16).  The total rank is padded with zero rows to a
+    multiple of 32.  Returns (D bf16 [R, K], U bf16 [N, R]) on ``device`` (the
+    first adapter's device by default), or None when R would exceed
+    ``MAX_LORA_RANK``.
+    """
+    pairs = list(pairs)
+    if not pairs:
+        return None
+    K = pairs[0][0].shape[1]
+    N = pairs[0][1].shape[0]
+    ranks = []
+    for down, up, _ in pairs:
+        if down.dim() != 2 or up.dim() != 2 or down.shape[1] != K or up.shape[0] != N \
+                or up.shape[1] != down.shape[0]:
+            raise ValueError(f"LoRA pair shapes down {tuple(down.shape)} up {tuple(up.shape)} "
+                             f"do not fit K={K} N={N}")
+        ranks.append(down.shape[0])
+    R = -(-sum(ranks) // 32) * 32
+    if R > MAX_LORA_RANK or R == 0:
+        return None
+    dev = device if device is not None else pairs[0][0].device
+    D = torch.zeros((R, K), dtype=torch.bfloat16, device=dev)
+    U = torch.zeros((N, R), dtype=torch.bfloat16, device=dev)
+    r0 = 0
+    for (down, up, scale), r in zip(pairs, ranks):
+        D[r0:r0 + r] = down.to(dev, torch.float32).to(torch.bfloat16)
+        U[:, r0:r0 + r] = (up.to(dev, torch.float32) * float(scale)).to(torch.bfloat16)
+        r0 += r
+    return D, U
 
 
 def convrot_w8a8_linear(x, qweight, wscales, bias=None, convrot_groupsize=256):

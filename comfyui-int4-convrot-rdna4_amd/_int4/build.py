@@ -14,7 +14,7 @@ import subprocess
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _PKG = os.path.dirname(_HERE)
 _CSRC = os.path.join(_PKG, "csrc")
-SOURCES = ("rotquant.hip", "gemm.hip", "capi.hip")
+SOURCES = ("rotquant.hip", "gemm.hip", "lora.hip", "capi.hip")
 HEADERS = ("common.h",)
 ARCH = "gfx950"
 

@@ -34,6 +34,8 @@ _SIGNATURES = {
     "ck_int4_convrot_gemm": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
     "cr_int4_convrot_gemm_ex": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
     "cr_convrot_quant_int4_stochastic": ([_vp, _i, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
+    "cr_lora_down": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
+    "cr_int4_convrot_gemm_lora": ([_vp] * 7 + [_i, ctypes.c_float, _vp] + [_i] * 4 + [_vp], _i),
     "cr_max_quant_k": ([], _i),
     "cr_abi_version": ([], _i),
 }
@@ -211,4 +213,47 @@ def int4_convrot_gemm(x_packed, w_packed, x_scale, w_scale, bias, out_dtype):
                                   _stream(x_packed.device))
     if rc != 0:
         raise RuntimeError(f"ck_int4_convrot_gemm failed, hipError={rc}")
+    return out
+
+
+def lora_down(x: torch.Tensor, down: torch.Tensor) -> torch.Tensor:
+    """t = bf16(x @ down^T) for the dynamic-LoRA side path.  x [M, K] bf16/f16,
+    down [R, K] bf16 with R in {32, 64, 96, 128} -> t [M, R] bf16."""
+    lib = load_library()
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"lora_down input must be bf16/f16, got {x.dtype}")
+    if down.dtype != torch.bfloat16:
+        raise ValueError("lora down weights must be bf16")
+    _check_cuda(x, down)
+    x = _aligned(x)
+    down = _aligned(down)
+    M, K = x.shape
+    R, K2 = down.shape
+    if K != K2:
+        raise ValueError(f"K mismatch: x {tuple(x.shape)} down {tuple(down.shape)}")
+    t = torch.empty((M, R), dtype=torch.bfloat16, device=x.device)
+    rc = lib.cr_lora_down(_ptr(x), _IN_DTYPE_CODE[x.dtype], _ptr(down), _ptr(t), M, K, R, _stream(x.device))
+    if rc != 0:
+        raise RuntimeError(f"cr_lora_down failed, hipError={rc}")
+    return t
+
+
+def int4_convrot_gemm_lora(x_packed, w_packed, x_scale, w_scale, bias, t, up, scale: float, epilogue: int):
+    """GEMM + dequant epilogue + scale * (t @ up^T); t [M, R], up [N, R] bf16."""
+    lib = load_library()
+    x_packed, w_packed, x_scale, w_scale, bias, M, N, K = _gemm_args(
+        x_packed, w_packed, x_scale, w_scale, bias)
+    _check_cuda(t, up)
+    t = _aligned(t)
+    up = _aligned(up)
+    R = t.shape[1]
+    if t.dtype != torch.bfloat16 or up.dtype != torch.bfloat16 or up.shape != (N, R) or t.shape[0] != M:
+        raise ValueError("lora operands: t [M, R] and up [N, R] bf16")
+    odt = {EPI_F32: torch.float32, EPI_BF16: torch.bfloat16, EPI_BF16_EAGER: torch.bfloat16}[epilogue]
+    out = torch.empty((M, N), dtype=odt, device=x_packed.device)
+    rc = lib.cr_int4_convrot_gemm_lora(_ptr(x_packed), _ptr(w_packed), _ptr(x_scale), _ptr(w_scale), _ptr(bias),
+                                       _ptr(t), _ptr(up), R, ctypes.c_float(scale), _ptr(out), M, N, K, epilogue,
+                                       _stream(x_packed.device))
+    if rc != 0:
+        raise RuntimeError(f"cr_int4_convrot_gemm_lora failed, hipError={rc}")
     return out

@@ -10,6 +10,11 @@ hipError_t rotquant_launch(const void* x, int in_dtype, const void* noise, int8_
 int rotquant_max_k();
 hipError_t gemm_launch(const int8_t* Xp, const int8_t* Wp, const float* xs, const float* ws,
                        const float* bias, void* out, int M, int N, int K, int epi, hipStream_t st);
+hipError_t gemm_lora_launch(const int8_t* Xp, const int8_t* Wp, const float* xs, const float* ws,
+                            const float* bias, const void* t, const void* U, int R, float scale, void* out,
+                            int M, int N, int K, int epi, hipStream_t st);
+hipError_t lora_down_launch(const void* x, int in_dtype, const void* D, void* t, int M, int K, int R,
+                            hipStream_t st);
 }  // namespace convrot
 
 #define API extern "C" __attribute__((visibility("default")))
@@ -59,6 +64,27 @@ API int ck_int4_convrot_gemm(const void* Xp, const void* Wp, const void* xscale,
     return cr_int4_convrot_gemm_ex(Xp, Wp, xscale, wscale, bias, out, M, N, K, out_dtype, stream);
 }
 
+static int lora_rank_ok(int R) { return R >= 32 && R <= 128 && R % 32 == 0; }
+
+API int cr_lora_down(const void* x, int in_dtype, const void* D, void* t, int M, int K, int R, void* stream) {
+    if ((in_dtype != 1 && in_dtype != 2) || M < 0 || K <= 0 || K % 16 != 0 || !lora_rank_ok(R)) return -1;
+    hipError_t e = convrot::lora_down_launch(x, in_dtype, D, t, M, K, R, reinterpret_cast<hipStream_t>(stream));
+    return (int)e;
+}
+
+API int cr_int4_convrot_gemm_lora(const void* Xp, const void* Wp, const void* xscale, const void* wscale,
+                                  const void* bias, const void* t, const void* U, int R, float scale,
+                                  void* out, int M, int N, int K, int epilogue, void* stream) {
+    if (K % 32 != 0 || K <= 0 || K >= 131072 || M < 0 || N < 0) return -1;
+    if (epilogue < 0 || epilogue > 2 || !lora_rank_ok(R) || t == nullptr || U == nullptr) return -1;
+    hipError_t e = convrot::gemm_lora_launch(reinterpret_cast<const int8_t*>(Xp), reinterpret_cast<const int8_t*>(Wp),
+                                             reinterpret_cast<const float*>(xscale),
+                                             reinterpret_cast<const float*>(wscale),
+                                             reinterpret_cast<const float*>(bias), t, U, R, scale, out, M, N, K,
+                                             epilogue, reinterpret_cast<hipStream_t>(stream));
+    return (int)e;
+}
+
 API int cr_max_quant_k(void) { return convrot::rotquant_max_k(); }
 
-API int cr_abi_version(void) { return 1; }
+API int cr_abi_version(void) { return 2; }

@@ -49,11 +49,88 @@ __device__ __forceinline__ void unpack16(uint4 p, v4i& lo_step, v4i& hi_step) {
 
 __device__ __forceinline__ float bf16r(float f) { return round_to_dt<DT_BF16>(f); }
 
-template <int EPI>
+// Optional fused dynamic-LoRA term: out += scale * t[m, :] . U[n, :] (rank R).
+struct LoraArgs {
+    const __bf16* t;      // [M, R] bf16 (x @ D^T, from lora_down)
+    const __bf16* U;      // [N, R] bf16
+    int R;                // multiple of 16 (0: no LoRA)
+    float scale;
+};
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// Epilogue of a wave's FMT x FNT grid of 32x32 accumulator tiles at (row0, col0).
+// 32x32 layout: lane l, register r -> col = l % 32, row = 8 (r / 4) + 4 (l / 32) + r % 4.
+// The LoRA product uses the same layout (bf16 MFMA over R), issued by the
+// whole wave before any per-lane bounds check.
+template <int EPI, int FMT, int FNT, bool LORA>
+__device__ __forceinline__ void epilogue_tiles(const v16i (&acc)[FMT][FNT], const float* __restrict__ xs,
+                                               const float* __restrict__ ws, const float* __restrict__ bias,
+                                               void* __restrict__ out, int M, int N, int row0, int col0,
+                                               int lane, const LoraArgs& la) {
+    const int h = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < FMT; ++i) {
+        const int rbase = row0 + i * 32 + 4 * h;
+        float xsv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = rbase + 8 * (r >> 2) + (r & 3);
+            xsv[r] = (EPI != EPI_ACC && row < M) ? xs[row] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < FNT; ++j) {
+            const int col = col0 + j * 32 + (lane & 31);
+            f32x16_t lacc = (f32x16_t){0};
+            if constexpr (LORA) {
+                const int trow = row0 + i * 32 + (lane & 31);          // MFMA A row of this lane
+                for (int rk = 0; rk < la.R; rk += 16) {
+                    const int k = rk + 8 * h;
+                    const bf16x8_t a = trow < M ? *reinterpret_cast<const bf16x8_t*>(la.t + (size_t)trow * la.R + k)
+                                                : (bf16x8_t){0};
+                    const bf16x8_t b = col < N ? *reinterpret_cast<const bf16x8_t*>(la.U + (size_t)col * la.R + k)
+                                               : (bf16x8_t){0};
+                    lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, lacc, 0, 0, 0);
+                }
+            }
+            if (col >= N) continue;
+            float wsc = 0.0f, bv = 0.0f;
+            if constexpr (EPI != EPI_ACC) {
+                wsc = ws[col];
+                if (bias) bv = bias[col];
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = rbase + 8 * (r >> 2) + (r & 3);
+                if (row >= M) continue;
+                const int a = acc[i][j][r] >> 8;
+                const size_t o = (size_t)row * N + col;
+                if constexpr (EPI == EPI_ACC) {
+                    reinterpret_cast<int32_t*>(out)[o] = a;
+                } else if constexpr (EPI == EPI_BF16_EAGER) {
+                    float v = bf16r(bf16r((float)a) * bf16r(xsv[r]));
+                    v = bf16r(v * bf16r(wsc));
+                    if (bias) v = bf16r(v + bf16r(bv));
+                    if constexpr (LORA) v = bf16r(v + bf16r(__fmul_rn(la.scale, lacc[r])));
+                    reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f32_to_bf16_bits(v);
+                } else {
+                    float v = __fmul_rn(__fmul_rn((float)a, xsv[r]), wsc);
+                    if (bias) v = __fadd_rn(v, bv);
+                    if constexpr (LORA) v = __fadd_rn(v, __fmul_rn(la.scale, lacc[r]));
+                    if constexpr (EPI == EPI_F32) reinterpret_cast<float*>(out)[o] = v;
+                    else reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f32_to_bf16_bits(v);
+                }
+            }
+        }
+    }
+}
+
+template <int EPI, bool LORA>
 __global__ __launch_bounds__(NTHR) void w4a4_gemm_kernel(
         const int8_t* __restrict__ Xp, const int8_t* __restrict__ Wp,
         const float* __restrict__ xs, const float* __restrict__ ws, const float* __restrict__ bias,
-        void* __restrict__ out, int M, int N, int K) {
+        void* __restrict__ out, int M, int N, int K, LoraArgs lora) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[2][(TBM + TBN) * LDS_STRIDE];
 
     const int tid = threadIdx.x;
@@ -142,41 +219,7 @@ __global__ __launch_bounds__(NTHR) void w4a4_gemm_kernel(
         __syncthreads();
     }
 
-    // epilogue: 32x32 accumulator layout, lane l / register r ->
-    //   col = l % 32, row = 8 * (r / 4) + 4 * (l / 32) + r % 4
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int col = n0 + wn * WTN + j * 32 + (lane & 31);
-            if (col >= N) continue;
-            float wsc = 0.0f, bv = 0.0f;
-            if constexpr (EPI != EPI_ACC) {
-                wsc = ws[col];
-                if (bias) bv = bias[col];
-            }
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row >= M) continue;
-                const int a = acc[i][j][r] >> 8;
-                const size_t o = (size_t)row * N + col;
-                if constexpr (EPI == EPI_ACC) {
-                    reinterpret_cast<int32_t*>(out)[o] = a;
-                } else if constexpr (EPI == EPI_BF16_EAGER) {
-                    float v = bf16r(bf16r((float)a) * bf16r(xs[row]));
-                    v = bf16r(v * bf16r(wsc));
-                    if (bias) v = bf16r(v + bf16r(bv));
-                    reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f32_to_bf16_bits(v);
-                } else {
-                    float v = __fmul_rn(__fmul_rn((float)a, xs[row]), wsc);
-                    if (bias) v = __fadd_rn(v, bv);
-                    if constexpr (EPI == EPI_F32) reinterpret_cast<float*>(out)[o] = v;
-                    else reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f32_to_bf16_bits(v);
-                }
-            }
-        }
-    }
+    epilogue_tiles<EPI, FM, FN, LORA>(acc, xs, ws, bias, out, M, N, m0 + wm * WTM, n0 + wn * WTN, lane, lora);
 }
 
 // ---------------------------------------------------------------------------
@@ -224,62 +267,11 @@ __device__ __forceinline__ int swz(int row, int chunk) {
 // outstanding (vmcnt split over bits 3:0 and 15:14; expcnt / lgkmcnt not waited)
 constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
-// Epilogue of a wave's FMT x FNT grid of 32x32 accumulator tiles at (row0, col0).
-// 32x32 layout: lane l, register r -> col = l % 32, row = 8 (r / 4) + 4 (l / 32) + r % 4.
-// The per-row scales of a tile are 4 groups of 4 contiguous rows, loaded once.
-template <int EPI, int FMT, int FNT>
-__device__ __forceinline__ void epilogue_tiles(const v16i (&acc)[FMT][FNT], const float* __restrict__ xs,
-                                               const float* __restrict__ ws, const float* __restrict__ bias,
-                                               void* __restrict__ out, int M, int N, int row0, int col0,
-                                               int lane) {
-    const int h = lane >> 5;
-#pragma unroll
-    for (int i = 0; i < FMT; ++i) {
-        const int rbase = row0 + i * 32 + 4 * h;
-        float xsv[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = rbase + 8 * (r >> 2) + (r & 3);
-            xsv[r] = (EPI != EPI_ACC && row < M) ? xs[row] : 0.0f;
-        }
-#pragma unroll
-        for (int j = 0; j < FNT; ++j) {
-            const int col = col0 + j * 32 + (lane & 31);
-            if (col >= N) continue;
-            float wsc = 0.0f, bv = 0.0f;
-            if constexpr (EPI != EPI_ACC) {
-                wsc = ws[col];
-                if (bias) bv = bias[col];
-            }
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = rbase + 8 * (r >> 2) + (r & 3);
-                if (row >= M) continue;
-                const int a = acc[i][j][r] >> 8;
-                const size_t o = (size_t)row * N + col;
-                if constexpr (EPI == EPI_ACC) {
-                    reinterpret_cast<int32_t*>(out)[o] = a;
-                } else if constexpr (EPI == EPI_BF16_EAGER) {
-                    float v = bf16r(bf16r((float)a) * bf16r(xsv[r]));
-                    v = bf16r(v * bf16r(wsc));
-                    if (bias) v = bf16r(v + bf16r(bv));
-                    reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f32_to_bf16_bits(v);
-                } else {
-                    float v = __fmul_rn(__fmul_rn((float)a, xsv[r]), wsc);
-                    if (bias) v = __fadd_rn(v, bv);
-                    if constexpr (EPI == EPI_F32) reinterpret_cast<float*>(out)[o] = v;
-                    else reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f32_to_bf16_bits(v);
-                }
-            }
-        }
-    }
-}
-
-template <int EPI, int WN>
+template <int EPI, int WN, bool LORA>
 __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
         const int8_t* __restrict__ Xp, const int8_t* __restrict__ Wp,
         const float* __restrict__ xs, const float* __restrict__ ws, const float* __restrict__ bias,
-        void* __restrict__ out, int M, int N, int K) {
+        void* __restrict__ out, int M, int N, int K, LoraArgs lora) {
     extern __shared__ __attribute__((aligned(16))) uint8_t plds[];
 
     constexpr int P_THREADS = 128 * WN;                 // 2 x WN waves
@@ -390,55 +382,57 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
         }
     }
 
-    epilogue_tiles<EPI, 4, PFN>(acc, xs, ws, bias, out, M, N, m0 + wm * 128, n0 + wn * WTN_P, lane);
+    epilogue_tiles<EPI, 4, PFN, LORA>(acc, xs, ws, bias, out, M, N, m0 + wm * 128, n0 + wn * WTN_P, lane, lora);
 }
 
-template <int EPI, int WN = CONVROT_PIPE_WN>
-static hipError_t pipe_launch(const int8_t* Xp, const int8_t* Wp, const float* xs, const float* ws,
-                              const float* bias, void* out, int M, int N, int K, hipStream_t st) {
-    const int ntiles = ((M + P_BM - 1) / P_BM) * ((N + P_BN - 1) / P_BN);
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_pipe_kernel<EPI, WN>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, P_STAGES * P_STAGE_BYTES);
-        if (e != hipSuccess) return e;
-        attr_set = true;
+template <int EPI, bool LORA>
+static hipError_t launch_epi(const int8_t* Xp, const int8_t* Wp, const float* xs, const float* ws,
+                             const float* bias, void* out, int M, int N, int K, const LoraArgs& la,
+                             hipStream_t st) {
+    if (K % P_BK == 0) {
+        constexpr int WN = CONVROT_PIPE_WN;
+        const int ntiles = ((M + P_BM - 1) / P_BM) * ((N + P_BN - 1) / P_BN);
+        static bool attr_set = false;
+        if (!attr_set) {
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_pipe_kernel<EPI, WN, LORA>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               P_STAGES * P_STAGE_BYTES);
+            if (e != hipSuccess) return e;
+            attr_set = true;
+        }
+        hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<EPI, WN, LORA>), dim3(ntiles), dim3(128 * WN),
+                           P_STAGES * P_STAGE_BYTES, st, Xp, Wp, xs, ws, bias, out, M, N, K, la);
+    } else {
+        dim3 grid((N + TBN - 1) / TBN, (M + TBM - 1) / TBM), block(NTHR);
+        hipLaunchKernelGGL((w4a4_gemm_kernel<EPI, LORA>), grid, block, 0, st, Xp, Wp, xs, ws, bias, out, M, N, K, la);
     }
-    hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<EPI, WN>), dim3(ntiles), dim3(128 * WN), P_STAGES * P_STAGE_BYTES, st,
-                       Xp, Wp, xs, ws, bias, out, M, N, K);
     return hipGetLastError();
 }
 
 hipError_t gemm_launch(const int8_t* Xp, const int8_t* Wp, const float* xs, const float* ws,
                        const float* bias, void* out, int M, int N, int K, int epi, hipStream_t st) {
     if (M == 0 || N == 0) return hipSuccess;
-    if (K % P_BK == 0) {
-        switch (epi) {
-            case EPI_F32: return pipe_launch<EPI_F32>(Xp, Wp, xs, ws, bias, out, M, N, K, st);
-            case EPI_BF16: return pipe_launch<EPI_BF16>(Xp, Wp, xs, ws, bias, out, M, N, K, st);
-            case EPI_BF16_EAGER: return pipe_launch<EPI_BF16_EAGER>(Xp, Wp, xs, ws, bias, out, M, N, K, st);
-            case EPI_ACC: return pipe_launch<EPI_ACC>(Xp, Wp, xs, ws, bias, out, M, N, K, st);
-            default: return hipErrorInvalidValue;
-        }
-    }
-    dim3 grid((N + TBN - 1) / TBN, (M + TBM - 1) / TBM), block(NTHR);
+    const LoraArgs none{nullptr, nullptr, 0, 0.0f};
     switch (epi) {
-        case EPI_F32:
-            hipLaunchKernelGGL(w4a4_gemm_kernel<EPI_F32>, grid, block, 0, st, Xp, Wp, xs, ws, bias, out, M, N, K);
-            break;
-        case EPI_BF16:
-            hipLaunchKernelGGL(w4a4_gemm_kernel<EPI_BF16>, grid, block, 0, st, Xp, Wp, xs, ws, bias, out, M, N, K);
-            break;
-        case EPI_BF16_EAGER:
-            hipLaunchKernelGGL(w4a4_gemm_kernel<EPI_BF16_EAGER>, grid, block, 0, st, Xp, Wp, xs, ws, bias, out, M, N, K);
-            break;
-        case EPI_ACC:
-            hipLaunchKernelGGL(w4a4_gemm_kernel<EPI_ACC>, grid, block, 0, st, Xp, Wp, xs, ws, bias, out, M, N, K);
-            break;
-        default:
-            return hipErrorInvalidValue;
+        case EPI_F32: return launch_epi<EPI_F32, false>(Xp, Wp, xs, ws, bias, out, M, N, K, none, st);
+        case EPI_BF16: return launch_epi<EPI_BF16, false>(Xp, Wp, xs, ws, bias, out, M, N, K, none, st);
+        case EPI_BF16_EAGER: return launch_epi<EPI_BF16_EAGER, false>(Xp, Wp, xs, ws, bias, out, M, N, K, none, st);
+        case EPI_ACC: return launch_epi<EPI_ACC, false>(Xp, Wp, xs, ws, bias, out, M, N, K, none, st);
+        default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
+}
+
+hipError_t gemm_lora_launch(const int8_t* Xp, const int8_t* Wp, const float* xs, const float* ws,
+                            const float* bias, const void* t, const void* U, int R, float scale, void* out,
+                            int M, int N, int K, int epi, hipStream_t st) {
+    if (M == 0 || N == 0) return hipSuccess;
+    const LoraArgs la{reinterpret_cast<const __bf16*>(t), reinterpret_cast<const __bf16*>(U), R, scale};
+    switch (epi) {
+        case EPI_F32: return launch_epi<EPI_F32, true>(Xp, Wp, xs, ws, bias, out, M, N, K, la, st);
+        case EPI_BF16: return launch_epi<EPI_BF16, true>(Xp, Wp, xs, ws, bias, out, M, N, K, la, st);
+        case EPI_BF16_EAGER: return launch_epi<EPI_BF16_EAGER, true>(Xp, Wp, xs, ws, bias, out, M, N, K, la, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace convrot

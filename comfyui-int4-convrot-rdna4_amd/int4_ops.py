@@ -62,6 +62,33 @@ def _patch_fields(patch):
     return v, offset, function, 1.0
 
 
+def _plain_lora(v, in_features, out_features):
+    """(down, up, scale) of a plain LoRA adapter, or None.
+
+    A plain LoRA (comfy's LoRAAdapter, ``name == "lora"``) holds
+    ``weights = (up [N, r], down [r, K], alpha, mid, dora_scale, reshape)`` and
+    its bypass adds ``multiplier * (alpha / r) * up(down(x))`` (reference
+    int4_ops.py:181-192).  Adapters with a mid tensor, a DoRA scale, a reshape
+    or shapes that do not fit the layer keep the generic ``h()`` side path."""
+    if getattr(v, "name", None) != "lora":
+        return None
+    w = getattr(v, "weights", None)
+    if not isinstance(w, (tuple, list)) or len(w) < 3:
+        return None
+    up, down, alpha = w[0], w[1], w[2]
+    if any(len(w) > i and w[i] is not None for i in (3, 4, 5)):
+        return None
+    if not (isinstance(up, torch.Tensor) and isinstance(down, torch.Tensor)):
+        return None
+    if down.dim() != 2 or up.dim() != 2:
+        return None
+    r = down.shape[0]
+    if down.shape[1] != in_features or up.shape != (out_features, r) or r == 0:
+        return None
+    a = float(alpha) if alpha is not None else float(r)
+    return down, up, float(getattr(v, "multiplier", 1.0)) * a / r
+
+
 def _parse_quant_tag(tag):
     """Decode a ComfyUI native ``<key>.comfy_quant`` uint8-JSON tag.
 
@@ -115,6 +142,8 @@ if _COMFY_OPS and _CK_OK:
                 self._qgs = None      # convrot groupsize
                 self._qmode = None    # "int4" | "int8" | None (bf16)
                 self._dyn_lora = None
+                self._dyn_fused = None   # (D, U) bf16: plain LoRAs fused into the GEMM epilogue
+                self._dyn_rest = None    # adapters that keep the generic h() side path
                 self.comfy_cast_weights = False
 
             _normalize_lora_key = staticmethod(_strip_prefix)
@@ -184,9 +213,27 @@ if _COMFY_OPS and _CK_OK:
                     prepared.append(v)
                 return prepared
 
-            def _apply_dyn_lora(self, x, out):
+            def _set_dyn_lora(self, prepared):
+                """Attach prepared adapters; the plain LoRAs among them are
+                concatenated into one (D, U) pair that the W4A4 GEMM applies in
+                its epilogue, the others keep their h() side path."""
+                self._dyn_lora = prepared
+                self._dyn_fused, self._dyn_rest = None, prepared
+                plain = [_plain_lora(v, self.in_features, self.out_features) for v in prepared]
+                if not any(p is not None for p in plain):
+                    return
+                try:
+                    fused = _ck.fuse_lora_pairs([p for p in plain if p is not None])
+                except Exception as e:
+                    logging.warning(f"INT4 ConvRot: LoRA fusion failed, using the side path: {e}")
+                    fused = None
+                if fused is not None:
+                    self._dyn_fused = fused
+                    self._dyn_rest = [v for v, p in zip(prepared, plain) if p is None]
+
+            def _apply_dyn_lora(self, x, out, adapters=None):
                 """out + sum of the attached adapters' h(x) (already scaled)."""
-                for v in self._dyn_lora or ():
+                for v in (self._dyn_lora if adapters is None else adapters) or ():
                     try:
                         out = out + v.h(x, out)
                     except Exception as e:
@@ -223,7 +270,7 @@ if _COMFY_OPS and _CK_OK:
                 if patches:
                     prepared = self._prepare_dyn_adapters(patches)
                     if prepared is not None:
-                        self._dyn_lora = prepared
+                        self._set_dyn_lora(prepared)
                         Int4ConvRotOps._applied_lora.add(nk)
 
             def _load_prequantized(self, state_dict, prefix, wkey, skey, w):
@@ -286,7 +333,7 @@ if _COMFY_OPS and _CK_OK:
                             and w.dtype != torch.int8 and self._should_quantize(prefix, w)):
                         prepared = self._prepare_dyn_adapters(wpatches)
                     if prepared is not None:
-                        self._dyn_lora = prepared
+                        self._set_dyn_lora(prepared)
                         Int4ConvRotOps._applied_lora.add(nk)
                     else:
                         if w is not None and w.dtype != torch.int8:
@@ -337,10 +384,13 @@ if _COMFY_OPS and _CK_OK:
                 if self._qmode == "int8":
                     out = _ck.convrot_w8a8_linear(x, self._q, self._qs, bias=bias,
                                                   convrot_groupsize=self._qgs)
-                else:
-                    out = _ck.convrot_w4a4_linear(x, self._q, self._qs, bias=bias,
-                                                  convrot_groupsize=self._qgs)
-                return self._apply_dyn_lora(x, out)
+                    return self._apply_dyn_lora(x, out)
+                fused = self._dyn_fused
+                if fused is not None and fused[0].device != x.device:
+                    fused = self._dyn_fused = (fused[0].to(x.device), fused[1].to(x.device))
+                out = _ck.convrot_w4a4_linear(x, self._q, self._qs, bias=bias,
+                                              convrot_groupsize=self._qgs, lora=fused)
+                return self._apply_dyn_lora(x, out, self._dyn_rest if fused is not None else None)
 
 else:  # comfy.ops or the backend unavailable
     Int4ConvRotOps = None

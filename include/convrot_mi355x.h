@@ -77,6 +77,28 @@ int cr_int4_convrot_gemm_ex(const void* Xp, const void* Wp, const void* xscale, 
 int cr_convrot_quant_int4_stochastic(const void* x, int in_dtype, const void* noise, void* qout,
                                      void* scaleout, int M, int K, int G, void* stream);
 
+/*
+ * Down projection of the dynamic-LoRA side path: t = bf16(x @ D^T).
+ *   x [M, K] bf16 (in_dtype 1) or f16 (2), D [R, K] bf16, t [M, R] bf16;
+ *   R in {32, 64, 96, 128}, K % 16 == 0.
+ * Together with cr_int4_convrot_gemm_lora it replaces the per-adapter
+ * v.h(x, out) side path of Int4ConvRotOps.Linear._apply_dyn_lora
+ * (reference int4_ops.py:181-192), which has no native counterpart there.
+ */
+int cr_lora_down(const void* x, int in_dtype, const void* D, void* t, int M, int K, int R, void* stream);
+
+/*
+ * cr_int4_convrot_gemm_ex (epilogue 0, 1 or 2) plus the LoRA up projection in
+ * the epilogue:  out = epilogue + scale * (t @ U^T), with t from cr_lora_down
+ * and U [N, R] bf16 (several adapters: D and U concatenated along R, each
+ * adapter's multiplier * alpha / rank folded into its rows of U).  The term is
+ * added in fp32 before the output rounding (epilogue 2: rounded to bf16 and
+ * added in the bf16 chain).
+ */
+int cr_int4_convrot_gemm_lora(const void* Xp, const void* Wp, const void* xscale, const void* wscale,
+                              const void* bias, const void* t, const void* U, int R, float scale,
+                              void* out, int M, int N, int K, int epilogue, void* stream);
+
 /* Largest K accepted by the quantization entry points. */
 int cr_max_quant_k(void);
 

@@ -12,6 +12,7 @@ import pytest
 import torch
 
 from conftest import ROOT, import_pkg
+from fake_comfy import install_fake_comfy
 
 
 def header_symbols():
@@ -38,7 +39,7 @@ def test_library_exports_every_declared_symbol(native):
 
 def test_library_queries_without_gpu(native):
     lib = native.load_library()
-    assert lib.cr_abi_version() == 1
+    assert lib.cr_abi_version() == 2
     assert lib.cr_max_quant_k() == 32768
 
 
@@ -54,6 +55,14 @@ def test_argument_errors_return_minus_one(native):
     assert lib.ck_int4_convrot_gemm(n, n, n, n, n, n, 4, 4, 64, 5, n) == -1  # out dtype
     assert lib.cr_int4_convrot_gemm_ex(n, n, n, n, n, n, 4, 4, 64, 9, n) == -1
     assert lib.cr_convrot_quant_int4_stochastic(n, 1, n, n, n, 4, 256, 256, n) == -1  # no noise
+    f = ctypes.c_float(1.0)
+    assert lib.cr_lora_down(n, 1, n, n, 4, 256, 48, n) == -1        # rank not a multiple of 32
+    assert lib.cr_lora_down(n, 1, n, n, 4, 256, 160, n) == -1       # rank above 128
+    assert lib.cr_lora_down(n, 0, n, n, 4, 256, 32, n) == -1        # f32 input
+    assert lib.cr_lora_down(n, 1, n, n, 4, 40, 32, n) == -1         # K % 16
+    assert lib.cr_int4_convrot_gemm_lora(n, n, n, n, n, n, n, 32, f, n, 4, 4, 64, 3, n) == -1  # acc dump
+    assert lib.cr_int4_convrot_gemm_lora(n, n, n, n, n, n, n, 32, f, n, 4, 4, 64, 0, n) == -1  # null t/U
+    assert lib.cr_int4_convrot_gemm_lora(n, n, n, n, n, n, n, 64, f, n, 4, 4, 48, 0, n) == -1  # K % 32
 
 
 def test_pick_groupsize(backend):
@@ -109,31 +118,6 @@ def test_dequantize_matches_oracle(backend, oracle, goldens):
 # ----------------------------------------------------------------------------
 # Int4ConvRotOps load-time logic with a fake comfy package
 # ----------------------------------------------------------------------------
-
-def install_fake_comfy():
-    if "comfy.ops" in sys.modules and getattr(sys.modules["comfy.ops"], "_FAKE", False):
-        return
-    comfy = types.ModuleType("comfy")
-    ops = types.ModuleType("comfy.ops")
-    ops._FAKE = True
-
-    class manual_cast:
-        class Linear(torch.nn.Linear):
-            comfy_cast_weights = True
-
-            def reset_parameters(self):
-                return None
-
-            def forward(self, x):
-                w = self.weight.to(x.device, x.dtype)
-                b = self.bias.to(x.device, x.dtype) if self.bias is not None else None
-                return torch.nn.functional.linear(x, w, b)
-
-    ops.manual_cast = manual_cast
-    comfy.ops = ops
-    sys.modules["comfy"] = comfy
-    sys.modules["comfy.ops"] = ops
-
 
 @pytest.fixture(scope="module")
 def ops_mod():
