@@ -36,6 +36,9 @@ _SIGNATURES = {
     "cr_convrot_quant_int4_stochastic": ([_vp, _i, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
     "cr_lora_down": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
     "cr_int4_convrot_gemm_lora": ([_vp] * 7 + [_i, ctypes.c_float, _vp] + [_i] * 4 + [_vp], _i),
+    "cr_int4_to_bf6": ([_vp, _vp, _i, _i, _vp], _i),
+    "cr_int4_convrot_gemm_bf6": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
+    "cr_int4_convrot_gemm_bf6_lora": ([_vp] * 7 + [_i, ctypes.c_float, _vp] + [_i] * 4 + [_vp], _i),
     "cr_max_quant_k": ([], _i),
     "cr_abi_version": ([], _i),
 }
@@ -256,4 +259,90 @@ def int4_convrot_gemm_lora(x_packed, w_packed, x_scale, w_scale, bias, t, up, sc
                                        _stream(x_packed.device))
     if rc != 0:
         raise RuntimeError(f"cr_int4_convrot_gemm_lora failed, hipError={rc}")
+    return out
+
+
+def bf6_rows(rows: int) -> int:
+    """Rows of a B6T operand buffer: the row count padded to a multiple of 256."""
+    return (rows + 255) // 256 * 256
+
+
+def int4_to_bf6(packed: torch.Tensor) -> torch.Tensor:
+    """Packed int4 [rows, K/2] -> B6T bf6 operand, uint8 [bf6_rows(rows), 3K/4] (K % 128 == 0).
+    The row padding holds zero codes; the logical row count travels with the scales."""
+    lib = load_library()
+    _check_cuda(packed)
+    if packed.dtype not in (torch.int8, torch.uint8) or packed.dim() != 2:
+        raise ValueError("packed int4 operand must be a 2-D int8 tensor")
+    packed = _aligned(packed)
+    rows, K = packed.shape[0], packed.shape[1] * 2
+    if K % 128 != 0:
+        raise ValueError(f"bf6 operands need K % 128 == 0, got K={K}")
+    out = torch.empty((bf6_rows(rows), K // 4 * 3), dtype=torch.uint8, device=packed.device)
+    rc = lib.cr_int4_to_bf6(_ptr(packed), _ptr(out), rows, K, _stream(packed.device))
+    if rc != 0:
+        raise RuntimeError(f"cr_int4_to_bf6 failed, hipError={rc}")
+    return out
+
+
+def _bf6_gemm_args(a6, w6, x_scale, w_scale, bias, M, N):
+    _check_cuda(a6, w6, x_scale, w_scale, bias)
+    if a6.dtype != torch.uint8 or w6.dtype != torch.uint8 or a6.dim() != 2 or w6.dim() != 2:
+        raise ValueError("bf6 operands must be 2-D uint8 tensors")
+    if a6.shape[1] != w6.shape[1] or a6.shape[1] % 96 != 0:
+        raise ValueError(f"bf6 operand widths {a6.shape[1]} / {w6.shape[1]} do not match a K % 128 == 0")
+    K = a6.shape[1] // 3 * 4
+    M = x_scale.numel() if M is None else M
+    N = w_scale.numel() if N is None else N
+    if a6.shape[0] != bf6_rows(M) or w6.shape[0] != bf6_rows(N):
+        raise ValueError(f"bf6 operands of {a6.shape[0]} / {w6.shape[0]} rows do not hold M={M} / N={N}")
+    xs = _aligned(x_scale.reshape(-1).to(torch.float32)) if x_scale is not None else None
+    wsc = _aligned(w_scale.reshape(-1).to(torch.float32)) if w_scale is not None else None
+    if (xs is not None and xs.numel() != M) or (wsc is not None and wsc.numel() != N):
+        raise ValueError("scale lengths do not match the operands")
+    b = None
+    if bias is not None:
+        b = _aligned(bias.reshape(-1).to(torch.float32))
+        if b.numel() != N:
+            raise ValueError("bias length does not match N")
+    return _aligned(a6), _aligned(w6), xs, wsc, b, M, N, K
+
+
+def int4_convrot_gemm_bf6(a6, w6, x_scale, w_scale, bias, epilogue: int, M=None, N=None):
+    """W4A4 GEMM on B6T operands (exact accumulators), epilogue 0..3 as
+    int4_convrot_gemm_ex.  M / N default to the scale lengths."""
+    lib = load_library()
+    a6, w6, xs, wsc, b, M, N, K = _bf6_gemm_args(a6, w6, x_scale, w_scale, bias, M, N)
+    odt = {EPI_F32: torch.float32, EPI_BF16: torch.bfloat16, EPI_BF16_EAGER: torch.bfloat16,
+           EPI_ACC: torch.int32}[epilogue]
+    out = torch.empty((M, N), dtype=odt, device=a6.device)
+    rc = lib.cr_int4_convrot_gemm_bf6(_ptr(a6), _ptr(w6), _ptr(xs), _ptr(wsc), _ptr(b), _ptr(out),
+                                      M, N, K, epilogue, _stream(a6.device))
+    if rc != 0:
+        raise RuntimeError(f"cr_int4_convrot_gemm_bf6 failed, hipError={rc}")
+    return out
+
+
+def int4_gemm_acc_bf6(a6, w6, M: int, N: int):
+    """int32 accumulators of the bf6 GEMM (exact)."""
+    return int4_convrot_gemm_bf6(a6, w6, None, None, None, EPI_ACC, M=M, N=N)
+
+
+def int4_convrot_gemm_bf6_lora(a6, w6, x_scale, w_scale, bias, t, up, scale: float, epilogue: int):
+    """int4_convrot_gemm_bf6 + scale * (t @ up^T) in the epilogue (0..2)."""
+    lib = load_library()
+    a6, w6, xs, wsc, b, M, N, K = _bf6_gemm_args(a6, w6, x_scale, w_scale, bias, None, None)
+    _check_cuda(t, up)
+    t = _aligned(t)
+    up = _aligned(up)
+    R = t.shape[1]
+    if t.dtype != torch.bfloat16 or up.dtype != torch.bfloat16 or up.shape != (N, R) or t.shape[0] != M:
+        raise ValueError("lora operands: t [M, R] and up [N, R] bf16")
+    odt = {EPI_F32: torch.float32, EPI_BF16: torch.bfloat16, EPI_BF16_EAGER: torch.bfloat16}[epilogue]
+    out = torch.empty((M, N), dtype=odt, device=a6.device)
+    rc = lib.cr_int4_convrot_gemm_bf6_lora(_ptr(a6), _ptr(w6), _ptr(xs), _ptr(wsc), _ptr(b), _ptr(t), _ptr(up),
+                                           R, ctypes.c_float(scale), _ptr(out), M, N, K, epilogue,
+                                           _stream(a6.device))
+    if rc != 0:
+        raise RuntimeError(f"cr_int4_convrot_gemm_bf6_lora failed, hipError={rc}")
     return out

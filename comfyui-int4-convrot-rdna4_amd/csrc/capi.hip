@@ -15,6 +15,10 @@ hipError_t gemm_lora_launch(const int8_t* Xp, const int8_t* Wp, const float* xs,
                             int M, int N, int K, int epi, hipStream_t st);
 hipError_t lora_down_launch(const void* x, int in_dtype, const void* D, void* t, int M, int K, int R,
                             hipStream_t st);
+hipError_t int4_to_bf6_launch(const void* src, void* dst, int rows, int K, hipStream_t st);
+hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, const float* ws, const float* bias,
+                           const void* t, const void* U, int R, float scale, void* out, int M, int N, int K,
+                           int epi, hipStream_t st);
 }  // namespace convrot
 
 #define API extern "C" __attribute__((visibility("default")))
@@ -83,6 +87,33 @@ API int cr_int4_convrot_gemm_lora(const void* Xp, const void* Wp, const void* xs
                                              reinterpret_cast<const float*>(bias), t, U, R, scale, out, M, N, K,
                                              epilogue, reinterpret_cast<hipStream_t>(stream));
     return (int)e;
+}
+
+static int bf6_k_ok(int K) { return K > 0 && K % 128 == 0 && K < 131072; }
+
+API int cr_int4_to_bf6(const void* src, void* dst, int rows, int K, void* stream) {
+    if (rows < 0 || !bf6_k_ok(K)) return -1;
+    return (int)convrot::int4_to_bf6_launch(src, dst, rows, K, reinterpret_cast<hipStream_t>(stream));
+}
+
+API int cr_int4_convrot_gemm_bf6(const void* A6, const void* W6, const void* xscale, const void* wscale,
+                                 const void* bias, void* out, int M, int N, int K, int epilogue, void* stream) {
+    if (!bf6_k_ok(K) || M < 0 || N < 0 || epilogue < 0 || epilogue > 3) return -1;
+    return (int)convrot::gemm_bf6_launch(A6, W6, reinterpret_cast<const float*>(xscale),
+                                         reinterpret_cast<const float*>(wscale),
+                                         reinterpret_cast<const float*>(bias), nullptr, nullptr, 0, 0.0f, out,
+                                         M, N, K, epilogue, reinterpret_cast<hipStream_t>(stream));
+}
+
+API int cr_int4_convrot_gemm_bf6_lora(const void* A6, const void* W6, const void* xscale, const void* wscale,
+                                      const void* bias, const void* t, const void* U, int R, float scale,
+                                      void* out, int M, int N, int K, int epilogue, void* stream) {
+    if (!bf6_k_ok(K) || M < 0 || N < 0 || epilogue < 0 || epilogue > 2) return -1;
+    if (!lora_rank_ok(R) || t == nullptr || U == nullptr) return -1;
+    return (int)convrot::gemm_bf6_launch(A6, W6, reinterpret_cast<const float*>(xscale),
+                                         reinterpret_cast<const float*>(wscale),
+                                         reinterpret_cast<const float*>(bias), t, U, R, scale, out, M, N, K,
+                                         epilogue, reinterpret_cast<hipStream_t>(stream));
 }
 
 API int cr_max_quant_k(void) { return convrot::rotquant_max_k(); }

@@ -54,4 +54,24 @@ __device__ __forceinline__ float round_f64_to_dt(double d) {
     }
 }
 
+// Order LDS accesses of the lanes of one wave: every lane's earlier LDS
+// writes are visible to every lane's later LDS reads.  A wave issues its LDS
+// operations in program order; the fences keep the compiler from moving LDS
+// accesses across this point.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16 pair (a in the low half), both rounded to nearest
+// even by one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    const bf16x2_t h = __builtin_convertvector((f32x2_t){a, b}, bf16x2_t);
+    return __builtin_bit_cast(uint32_t, h);
+}
+
 }  // namespace convrot

@@ -22,14 +22,9 @@
 // padded to 80 bytes so every 8-lane phase of a ds_read_b128 hits distinct
 // banks), double-buffered, one barrier per block.
 
-#include "common.h"
+#include "gemm_common.h"
 
 namespace convrot {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
-
-enum : int { EPI_F32 = 0, EPI_BF16 = 1, EPI_BF16_EAGER = 2, EPI_ACC = 3 };
 
 constexpr int TBM = 256, TBN = 256;  // workgroup tile
 constexpr int TBK = 128;             // k values per LDS block
@@ -45,85 +40,6 @@ __device__ __forceinline__ void unpack16(uint4 p, v4i& lo_step, v4i& hi_step) {
                     (int)((p.y << 4) & 0xF0F0F0F0u), (int)(p.y & 0xF0F0F0F0u)};
     hi_step = (v4i){(int)((p.z << 4) & 0xF0F0F0F0u), (int)(p.z & 0xF0F0F0F0u),
                     (int)((p.w << 4) & 0xF0F0F0F0u), (int)(p.w & 0xF0F0F0F0u)};
-}
-
-__device__ __forceinline__ float bf16r(float f) { return round_to_dt<DT_BF16>(f); }
-
-// Optional fused dynamic-LoRA term: out += scale * t[m, :] . U[n, :] (rank R).
-struct LoraArgs {
-    const __bf16* t;      // [M, R] bf16 (x @ D^T, from lora_down)
-    const __bf16* U;      // [N, R] bf16
-    int R;                // multiple of 16 (0: no LoRA)
-    float scale;
-};
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-
-// Epilogue of a wave's FMT x FNT grid of 32x32 accumulator tiles at (row0, col0).
-// 32x32 layout: lane l, register r -> col = l % 32, row = 8 (r / 4) + 4 (l / 32) + r % 4.
-// The LoRA product uses the same layout (bf16 MFMA over R), issued by the
-// whole wave before any per-lane bounds check.
-template <int EPI, int FMT, int FNT, bool LORA>
-__device__ __forceinline__ void epilogue_tiles(const v16i (&acc)[FMT][FNT], const float* __restrict__ xs,
-                                               const float* __restrict__ ws, const float* __restrict__ bias,
-                                               void* __restrict__ out, int M, int N, int row0, int col0,
-                                               int lane, const LoraArgs& la) {
-    const int h = lane >> 5;
-#pragma unroll
-    for (int i = 0; i < FMT; ++i) {
-        const int rbase = row0 + i * 32 + 4 * h;
-        float xsv[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = rbase + 8 * (r >> 2) + (r & 3);
-            xsv[r] = (EPI != EPI_ACC && row < M) ? xs[row] : 0.0f;
-        }
-#pragma unroll
-        for (int j = 0; j < FNT; ++j) {
-            const int col = col0 + j * 32 + (lane & 31);
-            f32x16_t lacc = (f32x16_t){0};
-            if constexpr (LORA) {
-                const int trow = row0 + i * 32 + (lane & 31);          // MFMA A row of this lane
-                for (int rk = 0; rk < la.R; rk += 16) {
-                    const int k = rk + 8 * h;
-                    const bf16x8_t a = trow < M ? *reinterpret_cast<const bf16x8_t*>(la.t + (size_t)trow * la.R + k)
-                                                : (bf16x8_t){0};
-                    const bf16x8_t b = col < N ? *reinterpret_cast<const bf16x8_t*>(la.U + (size_t)col * la.R + k)
-                                               : (bf16x8_t){0};
-                    lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, lacc, 0, 0, 0);
-                }
-            }
-            if (col >= N) continue;
-            float wsc = 0.0f, bv = 0.0f;
-            if constexpr (EPI != EPI_ACC) {
-                wsc = ws[col];
-                if (bias) bv = bias[col];
-            }
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = rbase + 8 * (r >> 2) + (r & 3);
-                if (row >= M) continue;
-                const int a = acc[i][j][r] >> 8;
-                const size_t o = (size_t)row * N + col;
-                if constexpr (EPI == EPI_ACC) {
-                    reinterpret_cast<int32_t*>(out)[o] = a;
-                } else if constexpr (EPI == EPI_BF16_EAGER) {
-                    float v = bf16r(bf16r((float)a) * bf16r(xsv[r]));
-                    v = bf16r(v * bf16r(wsc));
-                    if (bias) v = bf16r(v + bf16r(bv));
-                    if constexpr (LORA) v = bf16r(v + bf16r(__fmul_rn(la.scale, lacc[r])));
-                    reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f32_to_bf16_bits(v);
-                } else {
-                    float v = __fmul_rn(__fmul_rn((float)a, xsv[r]), wsc);
-                    if (bias) v = __fadd_rn(v, bv);
-                    if constexpr (LORA) v = __fadd_rn(v, __fmul_rn(la.scale, lacc[r]));
-                    if constexpr (EPI == EPI_F32) reinterpret_cast<float*>(out)[o] = v;
-                    else reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f32_to_bf16_bits(v);
-                }
-            }
-        }
-    }
 }
 
 template <int EPI, bool LORA>
@@ -249,23 +165,7 @@ constexpr int P_ROWB = P_BK / 2;                       // 64 packed bytes per ro
 #endif
 constexpr int P_STAGES = CONVROT_PIPE_STAGES;
 constexpr int P_STAGE_BYTES = (P_BM + P_BN) * P_ROWB;  // 32 KB
-
-#ifndef CONVROT_SWZ64
-#define CONVROT_SWZ64 1
-#endif
-// chunk swizzle: row r stores its logical chunk c at physical chunk c ^ f(r).
-// With 64-byte rows a 16-byte read of chunk c by rows r..r+15 is conflict-free
-// when (r & 3, f(r)) takes 16 distinct values (64 banks x 4 B, 16 lanes per
-// phase) and when (r & 1, f(r)) takes 8 distinct values over r..r+7 (32 banks,
-// 8 lanes per phase); f = (bit1 ^ bit3) | bit2 << 1 satisfies both.
-__device__ __forceinline__ int swz(int row, int chunk) {
-    if (CONVROT_SWZ64) return chunk ^ ((((row >> 1) ^ (row >> 3)) & 1) | ((row >> 1) & 2));
-    return chunk ^ ((row >> 1) & 3);
-}
-
-// s_waitcnt immediate that waits until at most n vector-memory operations are
-// outstanding (vmcnt split over bits 3:0 and 15:14; expcnt / lgkmcnt not waited)
-constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+constexpr int P_LDS_BYTES = P_STAGES * P_STAGE_BYTES + EPI_SCALE_FLOATS * 4;
 
 template <int EPI, int WN, bool LORA>
 __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
@@ -294,6 +194,8 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
     const int n0 = (b / tiles_m) * P_BN;
     const int Kb = K / 2;
     const int nkb = K / P_BK;
+    float* sc = reinterpret_cast<float*>(plds + P_STAGES * P_STAGE_BYTES);
+    stage_scales(sc, xs, ws, bias, M, N, m0, n0, tid, 128 * WN);   // visible after the loop's first barrier
 
     // DMA source rows / chunks for this lane's P_LOADS instructions (fixed per tile)
     const int8_t* src[P_LOADS];
@@ -310,21 +212,11 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
             src[j] = Wp + (size_t)gn * Kb + c * 16;
         }
     }
-    // The DMA is issued from inline asm so the compiler does not add its own
-    // conservative vmcnt(0) before every LDS read; the explicit waits below
-    // (each lane waits for its own loads before the barrier that publishes a
-    // stage) are the only synchronisation.  LDS address of lane i = m0 + 16 i.
     const uint32_t lds_base = (uint32_t)(uintptr_t)plds;
     auto issue = [&](int kb) {
         const uint32_t st = lds_base + (kb % P_STAGES) * P_STAGE_BYTES + wave * P_LOADS * 1024;
 #pragma unroll
-        for (int j = 0; j < P_LOADS; ++j) {
-            const uint32_t m0v = __builtin_amdgcn_readfirstlane(st + j * 1024);
-            asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
-                         :
-                         : "s"(m0v), "v"(src[j] + kb * P_ROWB)
-                         : "memory", "m0");
-        }
+        for (int j = 0; j < P_LOADS; ++j) dma16(st + j * 1024, src[j] + kb * P_ROWB);
     };
 
     v16i acc[4][PFN];
@@ -340,9 +232,8 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
     for (int p = 0; p < P_STAGES - 1; ++p)
         if (p < nkb) issue(p);
     for (int kb = 0; kb < nkb; ++kb) {
-        // block kb landed: only the newer blocks' P_LOADS-per-block may stay in flight
-        if (kb + 1 < nkb) __builtin_amdgcn_s_waitcnt(vmcnt_imm((P_STAGES - 2) * P_LOADS));
-        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        // block kb landed (blocks kb+1 .. min(kb+P_STAGES-2, nkb-1) may stay in flight)
+        wait_block_landed<P_STAGES - 2, P_LOADS>(min(P_STAGES - 2, nkb - 1 - kb));
         __syncthreads();
         if (kb + P_STAGES - 1 < nkb) issue(kb + P_STAGES - 1);
         const uint8_t* la = plds + (kb % P_STAGES) * P_STAGE_BYTES;
@@ -373,16 +264,19 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < PFN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_lo[i], b_lo[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b_lo[j], a_lo[i], acc[i][j], 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < PFN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_hi[i], b_hi[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b_hi[j], a_hi[i], acc[i][j], 0, 0, 0);
         }
     }
 
-    epilogue_tiles<EPI, 4, PFN, LORA>(acc, xs, ws, bias, out, M, N, m0 + wm * 128, n0 + wn * WTN_P, lane, lora);
+    __syncthreads();                                     // every wave is done with the stages
+    constexpr int SCR = P_STAGES * P_STAGE_BYTES / (2 * WN);
+    epilogue_lds<EPI, 4, PFN, LORA, SCR>(acc, sc, bias != nullptr, out, M, N, m0, n0, m0 + wm * 128,
+                                         n0 + wn * WTN_P, lane, lora, plds + wave * SCR);
 }
 
 template <int EPI, bool LORA>
@@ -392,16 +286,20 @@ static hipError_t launch_epi(const int8_t* Xp, const int8_t* Wp, const float* xs
     if (K % P_BK == 0) {
         constexpr int WN = CONVROT_PIPE_WN;
         const int ntiles = ((M + P_BM - 1) / P_BM) * ((N + P_BN - 1) / P_BN);
-        static bool attr_set = false;
-        if (!attr_set) {
-            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_pipe_kernel<EPI, WN, LORA>),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               P_STAGES * P_STAGE_BYTES);
+        constexpr int kMaxDev = 64;
+        static bool attr_set[kMaxDev] = {};
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+        if (dev < 0 || dev >= kMaxDev) return hipErrorInvalidDevice;
+        if (!attr_set[dev]) {
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_pipe_kernel<EPI, WN, LORA>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, P_LDS_BYTES);
             if (e != hipSuccess) return e;
-            attr_set = true;
+            attr_set[dev] = true;
         }
         hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<EPI, WN, LORA>), dim3(ntiles), dim3(128 * WN),
-                           P_STAGES * P_STAGE_BYTES, st, Xp, Wp, xs, ws, bias, out, M, N, K, la);
+                           P_LDS_BYTES, st, Xp, Wp, xs, ws, bias, out, M, N, K, la);
     } else {
         dim3 grid((N + TBN - 1) / TBN, (M + TBM - 1) / TBM), block(NTHR);
         hipLaunchKernelGGL((w4a4_gemm_kernel<EPI, LORA>), grid, block, 0, st, Xp, Wp, xs, ws, bias, out, M, N, K, la);

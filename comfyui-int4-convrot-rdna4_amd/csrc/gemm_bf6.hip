@@ -1,0 +1,306 @@
+// W4A4 GEMM on the bf6 matrix cores of gfx950, with bit-exact accumulators.
+//
+// CDNA4 has no int4 matrix instruction, but its v_mfma_scale_f32_32x32x64_f8f6f4
+// runs 6-bit float operands at twice the int8 rate, and BF6 (E3M2, exponent
+// bias 3) represents every int4 value -8..7 exactly.  Products of two such
+// values are integers of magnitude <= 64, and every partial sum of a K-term dot
+// product is an integer of magnitude <= 64 K < 2^24 for K < 262144, so the fp32
+// accumulation is exact in any order: the accumulators equal the int32 ones of
+// the reference int4 GEMM bit for bit, and the epilogues are the int8 kernels'
+// (gemm_common.h).  With unit block scales (E8M0 127) the scale operands are
+// exact multiplications by 1.
+//
+// Operand format ("B6T", produced by int4_to_bf6t_kernel from the packed int4
+// layout, or directly by the fused rotate+quant kernel): a matrix [rows, K]
+// with K % 128 == 0, rows padded to a multiple of 256 (padding rows hold
+// zero codes), stored tile-major as [rows/256][K/128] chunks of 24576 bytes.
+// The chunk of (row tile, 128-k block) is exactly one operand half of an LDS
+// pipeline stage, so the GEMM copies it with 1 KB contiguous DMA instructions:
+//   bytes     0..16383  P part: row r at r*64, 16-byte chunk p holds dwords 0..3
+//                       of group p ^ f(r) (f: the swz() row function)
+//   bytes 16384..24575  Q part: row r at 16384 + r*32, 8-byte slot s holds
+//                       dwords 4..5 of group s ^ ((r >> 3) & 3)
+// where group g is the MFMA operand of k = 128 kb + 32 g .. +31: 32 BF6 codes,
+// code e in bits 6e .. 6e+5 of the 6-dword little-endian bit stream (the
+// operand layout of the instruction: lane l supplies row l % 32, k half l / 32).
+// Both permutations make the fragment reads bank-conflict-free.
+
+#include "gemm_common.h"
+
+namespace convrot {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// BF6 code of an integer -8..7: 0 -> 0, |q| = 2^e (1 + m/4) -> (e + 3) << 2 | m, sign 0x20.
+constexpr uint32_t bf6_code_of_int(int q) {
+    if (q == 0) return 0;
+    const int a = q < 0 ? -q : q;
+    int e = 0;
+    while ((a >> (e + 1)) != 0) ++e;
+    const int m = ((a << 2) >> e) & 3;
+    return (q < 0 ? 0x20u : 0u) | (uint32_t)((e + 3) << 2) | (uint32_t)m;
+}
+// codes of nibbles base .. base+7 (two's complement int4), 6 bits each
+constexpr uint64_t bf6_nibble_table(int base) {
+    uint64_t t = 0;
+    for (int i = 0; i < 8; ++i) {
+        const int n = base + i;
+        t |= (uint64_t)bf6_code_of_int(n >= 8 ? n - 16 : n) << (6 * i);
+    }
+    return t;
+}
+static_assert(bf6_code_of_int(7) == 23 && bf6_code_of_int(-8) == 56 && bf6_code_of_int(3) == 18, "bf6");
+
+__device__ __forceinline__ uint32_t bf6_of_nibble(uint32_t n) {
+    constexpr uint64_t LO = bf6_nibble_table(0), HI = bf6_nibble_table(8);
+    const uint64_t t = (n & 8) ? HI : LO;
+    return (uint32_t)(t >> ((n & 7) * 6)) & 63u;
+}
+
+// 32 packed nibbles (element e = nibble e of the 16 bytes, low nibble first)
+// -> one 6-dword bf6 operand
+__device__ __forceinline__ void encode_group(uint4 p, uint32_t (&d)[6]) {
+    const uint32_t w[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+    for (int i = 0; i < 6; ++i) d[i] = 0;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+        const uint32_t code = bf6_of_nibble((w[e >> 3] >> ((e & 7) * 4)) & 15u);
+        const int bit = 6 * e;
+        d[bit >> 5] |= code << (bit & 31);
+        if ((bit & 31) > 26) d[(bit >> 5) + 1] |= code >> (32 - (bit & 31));
+    }
+}
+
+constexpr int B6_CHUNK = 24576;          // bytes of one (256-row tile, 128-k block) chunk
+constexpr int B6_QOFF = 16384;           // Q part offset inside a chunk
+
+// packed int4 [rows, K/2] -> B6T; one thread per (row, 128-k block) of the
+// padded matrix, consecutive threads on consecutive rows of one chunk.
+__global__ __launch_bounds__(256) void int4_to_bf6t_kernel(const uint8_t* __restrict__ src,
+                                                           uint8_t* __restrict__ dst, int rows, int K) {
+    const int nkb = K / 128;
+    const long long id = (long long)blockIdx.x * 256 + threadIdx.x;
+    const int tiles = (rows + 255) / 256;
+    if (id >= (long long)tiles * nkb * 256) return;
+    const int r = (int)(id & 255);
+    const long long tk = id >> 8;                        // tile * nkb + kb
+    const int tile = (int)(tk / nkb), kb = (int)(tk % nkb);
+    const int row = tile * 256 + r;
+    uint4 in[4] = {};
+    if (row < rows) {
+        const uint4* s = reinterpret_cast<const uint4*>(src + (size_t)row * (K / 2) + (size_t)kb * 64);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) in[g] = s[g];
+    }
+    uint8_t* d = dst + (size_t)tk * B6_CHUNK;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        uint32_t c[6];
+        encode_group(in[g], c);
+        *reinterpret_cast<uint4*>(d + r * 64 + swz(r, g) * 16) = make_uint4(c[0], c[1], c[2], c[3]);
+        *reinterpret_cast<uint2*>(d + B6_QOFF + r * 32 + 8 * (g ^ ((r >> 3) & 3))) = make_uint2(c[4], c[5]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GEMM: 256 x 256 tile per workgroup of 8 waves (2 along M x 4 along N, wave
+// tile 128 x 64 = 4 x 2 MFMA tiles of 32 x 32).  A stage is the A chunk and
+// the B chunk of one 128-k block (48 KB), copied by global_load_lds_dwordx4
+// (6 contiguous 1 KB instructions per wave), three stages deep.  Per block
+// and wave: 2 k steps x 8 MFMAs, each operand one ds_read_b128 (P part) + one
+// ds_read_b64 (Q part).  The epilogue goes through LDS (epilogue_lds).
+// ---------------------------------------------------------------------------
+
+constexpr int B6_BM = 256, B6_BN = 256;
+constexpr int B6_THREADS = 512;
+constexpr int B6_STAGES = 3;
+constexpr int B6_STAGE_BYTES = 2 * B6_CHUNK;              // A chunk + B chunk: 48 KB
+constexpr int B6_LOADS = B6_STAGE_BYTES / 16 / B6_THREADS; // 6 DMA instructions per lane
+constexpr int B6_RING_BYTES = B6_STAGES * B6_STAGE_BYTES;  // 144 KB
+constexpr int B6_LDS_BYTES = B6_RING_BYTES + EPI_SCALE_FLOATS * 4;
+constexpr int BF6_FMT = 3;                                 // f8f6f4 operand format code of BF6 (E3M2)
+constexpr int E8M0_ONE = 127;                              // block scale 2^0
+
+__device__ __forceinline__ v8i bf6_operand(uint4 p, uint2 q) {
+    return (v8i){(int)p.x, (int)p.y, (int)p.z, (int)p.w, (int)q.x, (int)q.y, 0, 0};
+}
+
+template <int EPI, bool LORA>
+__global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
+        const uint8_t* __restrict__ A6, const uint8_t* __restrict__ W6,
+        const float* __restrict__ xs, const float* __restrict__ ws, const float* __restrict__ bias,
+        void* __restrict__ out, int M, int N, int K, LoraArgs lora) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds6[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 2, wn = wave & 3;
+    const int tiles_m = (M + B6_BM - 1) / B6_BM;
+    const int ntiles = tiles_m * ((N + B6_BN - 1) / B6_BN);
+    // XCD-aware renumbering: workgroup b runs on XCD b % 8
+    int b = blockIdx.x;
+    {
+        const int per = ntiles / 8, rem = ntiles % 8, x = b % 8, l = b / 8;
+        b = x * per + min(x, rem) + l;
+    }
+    const int m0 = (b % tiles_m) * B6_BM;
+    const int n0 = (b / tiles_m) * B6_BN;
+    const int nkb = K / 128;
+
+    float* sc = reinterpret_cast<float*>(lds6 + B6_RING_BYTES);
+    stage_scales(sc, xs, ws, bias, M, N, m0, n0, tid, B6_THREADS);   // visible after the loop's first barrier
+
+    // waves 0..3 copy the A chunk of a block, waves 4..7 the B chunk (6 KB each)
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const uint8_t* my_chunks = wave_u < 4 ? A6 + (size_t)(m0 / B6_BM) * nkb * B6_CHUNK
+                                          : W6 + (size_t)(n0 / B6_BN) * nkb * B6_CHUNK;
+    const uint8_t* my_src = my_chunks + (wave_u & 3) * (B6_LOADS * 1024) + lane * 16;
+    const uint32_t my_lds = (uint32_t)(uintptr_t)lds6 + wave_u * (B6_LOADS * 1024);
+    auto issue = [&](int kb) {
+        const uint32_t st = my_lds + (kb % B6_STAGES) * B6_STAGE_BYTES;
+        const uint8_t* src = my_src + (size_t)kb * B6_CHUNK;
+#pragma unroll
+        for (int j = 0; j < B6_LOADS; ++j) dma16(st + j * 1024, src + j * 1024);
+    };
+
+    v16f acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (v16f){0};
+
+    const int frow = lane & 31;
+    const int fhalf = lane >> 5;
+    // Per-lane byte offsets of this lane's fragments inside a stage, for the two
+    // k steps (group g = 2 s2 + half).  The P-chunk swizzle and the Q-slot
+    // permutation depend only on row bits 1..4, so the fragments of row tiles
+    // i = 1..3 sit at fixed distances (i * 2048 in P, i * 1024 in Q).
+    uint32_t offPa[2], offQa[2], offPb[2], offQb[2];
+    {
+        const int ra = wm * 128 + frow, rb = wn * 64 + frow;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const int g = 2 * s2 + fhalf;
+            offPa[s2] = ra * 64 + swz(ra, g) * 16;
+            offQa[s2] = B6_QOFF + ra * 32 + 8 * (g ^ ((ra >> 3) & 3));
+            offPb[s2] = B6_CHUNK + rb * 64 + swz(rb, g) * 16;
+            offQb[s2] = B6_CHUNK + B6_QOFF + rb * 32 + 8 * (g ^ ((rb >> 3) & 3));
+        }
+    }
+    // one 128-k block from the stage the offsets currently point into: all 12
+    // fragment reads first (both k steps), then the 16 MFMAs, so the second
+    // step's reads complete under the first step's MFMAs
+    auto compute = [&]() {
+        v8i fa[2][4], fb[2][2];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                fa[s2][i] = bf6_operand(*reinterpret_cast<const uint4*>(lds6 + offPa[s2] + i * 2048),
+                                        *reinterpret_cast<const uint2*>(lds6 + offQa[s2] + i * 1024));
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                fb[s2][j] = bf6_operand(*reinterpret_cast<const uint4*>(lds6 + offPb[s2] + j * 2048),
+                                        *reinterpret_cast<const uint2*>(lds6 + offQb[s2] + j * 1024));
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(   // transposed tile
+                            fb[s2][j], fa[s2][i], acc[i][j], BF6_FMT, BF6_FMT, 0, E8M0_ONE, 0, E8M0_ONE);
+#ifndef CONVROT_BF6_NO_SCHED
+        // keep that order: the scheduler would otherwise read each fragment just before its MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 18, 0);   // DS reads
+        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);   // MFMAs
+#endif
+    };
+
+#pragma unroll
+    for (int p = 0; p < B6_STAGES - 1; ++p)
+        if (p < nkb) issue(p);
+    for (int kb = 0; kb < nkb; ++kb) {
+        // block kb landed (blocks kb+1 .. min(kb+B6_STAGES-2, nkb-1) may stay in flight)
+        wait_block_landed<B6_STAGES - 2, B6_LOADS>(min(B6_STAGES - 2, nkb - 1 - kb));
+        __syncthreads();
+        if (kb + B6_STAGES - 1 < nkb) issue(kb + B6_STAGES - 1);
+        compute();
+        // advance the fragment offsets to the next stage of the ring (wave-uniform delta)
+        const uint32_t delta = (kb % B6_STAGES == B6_STAGES - 1) ? (uint32_t)(-(B6_STAGES - 1) * B6_STAGE_BYTES)
+                                                                 : (uint32_t)B6_STAGE_BYTES;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            offPa[s2] += delta; offQa[s2] += delta; offPb[s2] += delta; offQb[s2] += delta;
+        }
+    }
+
+    __syncthreads();                                     // every wave is done with the stages
+    // keep the epilogue's index arithmetic out of the main loop's registers
+    int em0 = m0, en0 = n0, elane = lane;
+    asm volatile("" : "+s"(M), "+s"(N), "+v"(em0), "+v"(en0), "+v"(elane));
+    constexpr int SCR = B6_RING_BYTES / (B6_THREADS / 64);
+    epilogue_lds<EPI, 4, 2, LORA, SCR>(acc, sc, bias != nullptr, out, M, N, em0, en0, em0 + wm * 128,
+                                       en0 + wn * 64, elane, lora, lds6 + wave * SCR);
+}
+
+template <int EPI, bool LORA>
+static hipError_t launch_bf6(const uint8_t* A6, const uint8_t* W6, const float* xs, const float* ws,
+                             const float* bias, void* out, int M, int N, int K, const LoraArgs& la,
+                             hipStream_t st) {
+    constexpr int kMaxDev = 64;
+    static bool attr_set[kMaxDev] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDev) return hipErrorInvalidDevice;
+    if (!attr_set[dev]) {
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_bf6_kernel<EPI, LORA>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, B6_LDS_BYTES);
+        if (e != hipSuccess) return e;
+        attr_set[dev] = true;
+    }
+    const int ntiles = ((M + B6_BM - 1) / B6_BM) * ((N + B6_BN - 1) / B6_BN);
+    hipLaunchKernelGGL((w4a4_gemm_bf6_kernel<EPI, LORA>), dim3(ntiles), dim3(B6_THREADS), B6_LDS_BYTES, st,
+                       A6, W6, xs, ws, bias, out, M, N, K, la);
+    return hipGetLastError();
+}
+
+hipError_t int4_to_bf6_launch(const void* src, void* dst, int rows, int K, hipStream_t st) {
+    if (rows == 0) return hipSuccess;
+    const long long n = (long long)((rows + 255) / 256) * (K / 128) * 256;
+    hipLaunchKernelGGL(int4_to_bf6t_kernel, dim3((unsigned)(n / 256)), dim3(256), 0, st,
+                       reinterpret_cast<const uint8_t*>(src), reinterpret_cast<uint8_t*>(dst), rows, K);
+    return hipGetLastError();
+}
+
+hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, const float* ws, const float* bias,
+                           const void* t, const void* U, int R, float scale, void* out, int M, int N, int K,
+                           int epi, hipStream_t st) {
+    if (M == 0 || N == 0) return hipSuccess;
+    const uint8_t* a = reinterpret_cast<const uint8_t*>(A6);
+    const uint8_t* w = reinterpret_cast<const uint8_t*>(W6);
+    if (t == nullptr) {
+        const LoraArgs none{nullptr, nullptr, 0, 0.0f};
+        switch (epi) {
+            case EPI_F32: return launch_bf6<EPI_F32, false>(a, w, xs, ws, bias, out, M, N, K, none, st);
+            case EPI_BF16: return launch_bf6<EPI_BF16, false>(a, w, xs, ws, bias, out, M, N, K, none, st);
+            case EPI_BF16_EAGER: return launch_bf6<EPI_BF16_EAGER, false>(a, w, xs, ws, bias, out, M, N, K, none, st);
+            case EPI_ACC: return launch_bf6<EPI_ACC, false>(a, w, xs, ws, bias, out, M, N, K, none, st);
+            default: return hipErrorInvalidValue;
+        }
+    }
+    const LoraArgs la{reinterpret_cast<const __bf16*>(t), reinterpret_cast<const __bf16*>(U), R, scale};
+    switch (epi) {
+        case EPI_F32: return launch_bf6<EPI_F32, true>(a, w, xs, ws, bias, out, M, N, K, la, st);
+        case EPI_BF16: return launch_bf6<EPI_BF16, true>(a, w, xs, ws, bias, out, M, N, K, la, st);
+        case EPI_BF16_EAGER: return launch_bf6<EPI_BF16_EAGER, true>(a, w, xs, ws, bias, out, M, N, K, la, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace convrot

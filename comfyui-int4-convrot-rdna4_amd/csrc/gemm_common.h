@@ -1,0 +1,278 @@
+// Pieces shared by the W4A4 GEMM kernels (int8 MFMA on packed nibbles in
+// gemm.hip, bf6 MFMA on pre-encoded operands in gemm_bf6.hip): the output
+// epilogues (with the optional fused LoRA term), the LDS chunk swizzle, the
+// global->LDS DMA issue and the pipeline waits.
+#pragma once
+
+#include "common.h"
+
+namespace convrot {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+enum : int { EPI_F32 = 0, EPI_BF16 = 1, EPI_BF16_EAGER = 2, EPI_ACC = 3 };
+
+__device__ __forceinline__ float bf16r(float f) { return round_to_dt<DT_BF16>(f); }
+
+// Optional fused dynamic-LoRA term: out += scale * t[m, :] . U[n, :] (rank R).
+struct LoraArgs {
+    const __bf16* t;      // [M, R] bf16 (x @ D^T, from lora_down)
+    const __bf16* U;      // [N, R] bf16
+    int R;                // multiple of 16 (0: no LoRA)
+    float scale;
+};
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// Accumulator of one output: the int8 kernels accumulate 256 * acc in int32
+// (operands are 16 * q), the bf6 kernels accumulate acc exactly in fp32
+// (integer products, |partial sums| < 2^24).
+__device__ __forceinline__ int acc_int(int v) { return v >> 8; }
+__device__ __forceinline__ int acc_int(float v) { return (int)v; }
+__device__ __forceinline__ float acc_float(int v) { return (float)(v >> 8); }
+__device__ __forceinline__ float acc_float(float v) { return v; }   // an exact integer already
+
+// Per-tile epilogue scales staged in LDS by the workgroup at kernel start:
+// xs of the tile's 256 rows, ws and bias of its 256 columns (0 outside M / N).
+constexpr int EPI_SCALE_FLOATS = 3 * 256;
+__device__ __forceinline__ void stage_scales(float* sc, const float* __restrict__ xs, const float* __restrict__ ws,
+                                             const float* __restrict__ bias, int M, int N, int m0, int n0,
+                                             int tid, int nthreads) {
+    for (int i = tid; i < EPI_SCALE_FLOATS; i += nthreads) {
+        const int part = i >> 8, k = i & 255;
+        float v = 0.0f;
+        if (part == 0) { if (xs && m0 + k < M) v = xs[m0 + k]; }
+        else if (part == 1) { if (ws && n0 + k < N) v = ws[n0 + k]; }
+        else { if (bias && n0 + k < N) v = bias[n0 + k]; }
+        sc[i] = v;
+    }
+}
+
+// Epilogue of a wave's FMT x FNT grid of 32x32 accumulator tiles at (row0, col0).
+// 32x32 layout: lane l, register r -> col = l % 32, row = 8 (r / 4) + 4 (l / 32) + r % 4.
+// The LoRA product uses the same layout (bf16 MFMA over R), issued by the
+// whole wave before any per-lane bounds check.
+template <int EPI, int FMT, int FNT, bool LORA, typename AccV>
+__device__ __forceinline__ void epilogue_tiles(const AccV (&acc)[FMT][FNT], const float* __restrict__ xs,
+                                               const float* __restrict__ ws, const float* __restrict__ bias,
+                                               void* __restrict__ out, int M, int N, int row0, int col0,
+                                               int lane, const LoraArgs& la) {
+    const int h = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < FMT; ++i) {
+        const int rbase = row0 + i * 32 + 4 * h;
+        float xsv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = rbase + 8 * (r >> 2) + (r & 3);
+            xsv[r] = (EPI != EPI_ACC && row < M) ? xs[row] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < FNT; ++j) {
+            const int col = col0 + j * 32 + (lane & 31);
+            f32x16_t lacc = (f32x16_t){0};
+            if constexpr (LORA) {
+                const int trow = row0 + i * 32 + (lane & 31);          // MFMA A row of this lane
+                for (int rk = 0; rk < la.R; rk += 16) {
+                    const int k = rk + 8 * h;
+                    const bf16x8_t a = trow < M ? *reinterpret_cast<const bf16x8_t*>(la.t + (size_t)trow * la.R + k)
+                                                : (bf16x8_t){0};
+                    const bf16x8_t b = col < N ? *reinterpret_cast<const bf16x8_t*>(la.U + (size_t)col * la.R + k)
+                                               : (bf16x8_t){0};
+                    lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, lacc, 0, 0, 0);
+                }
+            }
+            if (col >= N) continue;
+            float wsc = 0.0f, bv = 0.0f;
+            if constexpr (EPI != EPI_ACC) {
+                wsc = ws[col];
+                if (bias) bv = bias[col];
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = rbase + 8 * (r >> 2) + (r & 3);
+                if (row >= M) continue;
+                const int a = acc_int(acc[i][j][r]);
+                const size_t o = (size_t)row * N + col;
+                if constexpr (EPI == EPI_ACC) {
+                    reinterpret_cast<int32_t*>(out)[o] = a;
+                } else if constexpr (EPI == EPI_BF16_EAGER) {
+                    float v = bf16r(bf16r((float)a) * bf16r(xsv[r]));
+                    v = bf16r(v * bf16r(wsc));
+                    if (bias) v = bf16r(v + bf16r(bv));
+                    if constexpr (LORA) v = bf16r(v + bf16r(__fmul_rn(la.scale, lacc[r])));
+                    reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f32_to_bf16_bits(v);
+                } else {
+                    float v = __fmul_rn(__fmul_rn((float)a, xsv[r]), wsc);
+                    if (bias) v = __fadd_rn(v, bv);
+                    if constexpr (LORA) v = __fadd_rn(v, __fmul_rn(la.scale, lacc[r]));
+                    if constexpr (EPI == EPI_F32) reinterpret_cast<float*>(out)[o] = v;
+                    else reinterpret_cast<uint16_t*>(out)[o] = (uint16_t)f32_to_bf16_bits(v);
+                }
+            }
+        }
+    }
+}
+
+// Epilogue through LDS for kernels that accumulate the TRANSPOSED tile
+// (MFMA with the B fragment as first operand): in a 32x32 accumulator lane l,
+// register r holds output row l % 32 and column 8 (r / 4) + 4 (l / 32) + r % 4,
+// so each lane owns 4 consecutive columns of one row per register quad.  The
+// values are computed as in epilogue_tiles, written to the wave's LDS scratch
+// in row-major order (one 8- or 16-byte write per quad; rows padded by 16
+// bytes), then copied out with one 16-byte store per lane and chunk so each
+// store instruction writes whole row segments.  Rows are processed in passes
+// of PT row tiles that fit SCR_BYTES.  `scr` must be 16-byte aligned and owned
+// by this wave; `sc` holds the workgroup tile's staged scales (stage_scales).
+template <int EPI, int FMT, int FNT, bool LORA, int SCR_BYTES, typename AccV>
+__device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const float* sc, bool has_bias,
+                                             void* __restrict__ out, int M, int N, int tile_m0, int tile_n0,
+                                             int row0, int col0, int lane, const LoraArgs& la, uint8_t* scr) {
+    constexpr int ES = (EPI == EPI_BF16 || EPI == EPI_BF16_EAGER) ? 2 : 4;
+    constexpr int RB = FNT * 32 * ES;                // bytes of one wave-tile row
+    constexpr int RS = RB + 16;                      // padded LDS row stride
+    constexpr int PT0 = SCR_BYTES / (32 * RS);
+    constexpr int PT = PT0 >= FMT ? FMT : (PT0 >= 2 ? 2 : 1);
+    static_assert(PT0 >= 1 && FMT % PT == 0, "scratch too small for one row tile");
+    constexpr int CW = RB / 16;                      // 16-byte chunks per row
+    constexpr int EPC = 16 / ES;                     // elements per chunk
+    const int h = lane >> 5;
+    const int l32 = lane & 31;
+    const bool vec = ((size_t)N * ES) % 16 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+#pragma unroll
+    for (int i0 = 0; i0 < FMT; i0 += PT) {
+#pragma unroll
+        for (int ii = 0; ii < PT; ++ii) {
+            const int i = i0 + ii;
+            const float xsv = sc[row0 - tile_m0 + i * 32 + l32];
+#pragma unroll
+            for (int j = 0; j < FNT; ++j) {
+                f32x16_t lacc = (f32x16_t){0};
+                if constexpr (LORA) {
+                    const int trow = row0 + i * 32 + l32;
+                    const int ucol = col0 + j * 32 + l32;
+                    for (int rk = 0; rk < la.R; rk += 16) {
+                        const int k = rk + 8 * h;
+                        const bf16x8_t a = trow < M ? *reinterpret_cast<const bf16x8_t*>(la.t + (size_t)trow * la.R + k)
+                                                    : (bf16x8_t){0};
+                        const bf16x8_t b = ucol < N ? *reinterpret_cast<const bf16x8_t*>(la.U + (size_t)ucol * la.R + k)
+                                                    : (bf16x8_t){0};
+                        lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, lacc, 0, 0, 0);   // transposed
+                    }
+                }
+                const int cbase = col0 - tile_n0 + j * 32 + 4 * h;       // first column of quad 0
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 w4 = *reinterpret_cast<const float4*>(sc + 256 + cbase + 8 * q);
+                    const float4 b4 = *reinterpret_cast<const float4*>(sc + 512 + cbase + 8 * q);
+                    const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+                    const float bvv[4] = {b4.x, b4.y, b4.z, b4.w};
+                    uint8_t* dst = scr + (ii * 32 + l32) * RS + (j * 32 + 8 * q + 4 * h) * ES;
+                    if constexpr (EPI == EPI_ACC) {
+                        *reinterpret_cast<int4*>(dst) = make_int4(acc_int(acc[i][j][4 * q]), acc_int(acc[i][j][4 * q + 1]),
+                                                                  acc_int(acc[i][j][4 * q + 2]), acc_int(acc[i][j][4 * q + 3]));
+                    } else {
+                        float v[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float a = acc_float(acc[i][j][4 * q + e]);
+                            if constexpr (EPI == EPI_BF16_EAGER) {
+                                float t = bf16r(bf16r(a) * bf16r(xsv));
+                                t = bf16r(t * bf16r(wv[e]));
+                                if (has_bias) t = bf16r(t + bf16r(bvv[e]));
+                                if constexpr (LORA) t = bf16r(t + bf16r(__fmul_rn(la.scale, lacc[4 * q + e])));
+                                v[e] = t;
+                            } else {
+                                float t = __fmul_rn(__fmul_rn(a, xsv), wv[e]);
+                                if (has_bias) t = __fadd_rn(t, bvv[e]);
+                                if constexpr (LORA) t = __fadd_rn(t, __fmul_rn(la.scale, lacc[4 * q + e]));
+                                v[e] = t;
+                            }
+                        }
+                        if constexpr (ES == 4) {
+                            *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+                        } else {
+                            *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                        }
+                    }
+                }
+            }
+        }
+        wave_sync();
+        constexpr int NCH = PT * 32 * CW;
+        constexpr int RSTEP = 64 / CW;                               // rows advanced per 64 chunks
+        const int cc = lane % CW;
+        const int col = col0 + cc * EPC;
+        const int rl0 = lane / CW;
+        uint8_t* orow = reinterpret_cast<uint8_t*>(out) + ((size_t)(row0 + i0 * 32 + rl0) * N + col) * ES;
+#pragma unroll
+        for (int q0 = 0; q0 < NCH; q0 += 64) {
+            const int rl = rl0 + (q0 / 64) * RSTEP;
+            const int row = row0 + i0 * 32 + rl;
+            uint8_t* o = orow + (size_t)(q0 / 64) * RSTEP * N * ES;
+            if (row < M && col < N) {
+                const uint4 d = *reinterpret_cast<const uint4*>(scr + rl * RS + cc * 16);
+                if (vec && col + EPC <= N) {
+                    *reinterpret_cast<uint4*>(o) = d;
+                } else {
+                    const uint32_t w[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+                    for (int e = 0; e < EPC; ++e) {
+                        if (col + e < N) {
+                            if constexpr (ES == 2) reinterpret_cast<uint16_t*>(o)[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+                            else reinterpret_cast<uint32_t*>(o)[e] = w[e];
+                        }
+                    }
+                }
+            }
+        }
+        wave_sync();
+    }
+}
+
+#ifndef CONVROT_SWZ64
+#define CONVROT_SWZ64 1
+#endif
+// chunk swizzle: row r stores its logical chunk c at physical chunk c ^ f(r).
+// With 64-byte rows a 16-byte read of chunk c by rows r..r+15 is conflict-free
+// when (r & 3, f(r)) takes 16 distinct values (64 banks x 4 B, 16 lanes per
+// phase) and when (r & 1, f(r)) takes 8 distinct values over r..r+7 (32 banks,
+// 8 lanes per phase); f = (bit1 ^ bit3) | bit2 << 1 satisfies both.
+__device__ __forceinline__ int swz(int row, int chunk) {
+    if (CONVROT_SWZ64) return chunk ^ ((((row >> 1) ^ (row >> 3)) & 1) | ((row >> 1) & 2));
+    return chunk ^ ((row >> 1) & 3);
+}
+
+// s_waitcnt immediate that waits until at most n vector-memory operations are
+// outstanding (vmcnt split over bits 3:0 and 15:14; expcnt / lgkmcnt not waited)
+constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
+
+// One 16-byte-per-lane global->LDS DMA (global_load_lds_dwordx4): lane i of
+// the wave writes lds_addr + 16 i.  Issued from inline asm so the compiler
+// adds no conservative vmcnt(0) of its own before later LDS reads; callers
+// synchronise with wait_block_landed + a barrier.
+__device__ __forceinline__ void dma16(uint32_t lds_addr, const void* src) {
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_addr);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(m0v), "v"(src)
+                 : "memory", "m0");
+}
+
+// Wait until this lane's DMA of the oldest in-flight block has landed, given
+// that `newer` younger blocks (LOADS instructions each) were issued after it.
+// vmcnt counts vector-memory operations completing in issue order, so waiting
+// for <= newer * LOADS outstanding is exactly "the oldest block is done".
+template <int MAXNEWER, int LOADS>
+__device__ __forceinline__ void wait_block_landed(int newer) {
+    static_assert(MAXNEWER <= 3 && MAXNEWER * LOADS <= 63, "vmcnt range");
+    if (MAXNEWER >= 3 && newer >= 3) __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * LOADS));
+    else if (MAXNEWER >= 2 && newer == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * LOADS));
+    else if (MAXNEWER >= 1 && newer == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(LOADS));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+}
+
+}  // namespace convrot

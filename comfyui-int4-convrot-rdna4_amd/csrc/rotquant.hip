@@ -334,14 +334,6 @@ __device__ __forceinline__ float held(const Held<DT>& h, int i) {
     else return f16bits_to_f32((i & 1) ? (h.w[i >> 1] >> 16) : h.w[i >> 1]);
 }
 
-__device__ __forceinline__ void wave_sync() {
-    // all lanes of a wave issue LDS operations in program order; keep the
-    // compiler from moving LDS accesses across this point
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // fp64 -> float with the bits below float precision folded into a sticky bit
 // (see round_f64_to_dt): rounding the result once to bf16/f16 equals rounding
 // the fp64 value once.  Monotone, so the max of jammed values rounds to the
@@ -355,13 +347,6 @@ __device__ __forceinline__ float jam_to_f32(double d) {
     return (float)__longlong_as_double((long long)((u & 0xffffffff00000000ull) | lo));
 }
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {   // both RNE in one v_cvt_pk_bf16_f32
-    const bf16x2_t h = __builtin_convertvector((f32x2_t){a, b}, bf16x2_t);
-    return __builtin_bit_cast(uint32_t, h);
-}
 
 template <int DT, int G, int NPMAX>
 __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(

@@ -99,6 +99,39 @@ int cr_int4_convrot_gemm_lora(const void* Xp, const void* Wp, const void* xscale
                               const void* bias, const void* t, const void* U, int R, float scale,
                               void* out, int M, int N, int K, int epilogue, void* stream);
 
+/*
+ * bf6 operand path.  CDNA4's v_mfma_scale_f32_32x32x64_f8f6f4 runs BF6 (E3M2)
+ * operands at twice the int8 rate and BF6 holds every int4 value exactly; the
+ * products are integers and the fp32 accumulation of a K < 131072 dot product
+ * is exact, so these entry points return the same accumulators (and, through
+ * the same epilogues, the same outputs) as cr_int4_convrot_gemm_ex.  They
+ * have no counterpart in the reference: the Linear replacement converts each
+ * weight once at load time and uses them on its forward path
+ * (reference _int4/__init__.py:94-138 is the call they serve).
+ *
+ * "B6T" layout of a [rows, K] operand (K % 128 == 0): rows padded to
+ * R = ceil(rows / 256) * 256 with zero codes; R * 3K/4 bytes stored as
+ * [R / 256][K / 128] chunks of 24576 bytes (256 rows x 128 k).  In a chunk,
+ * row r holds 64 bytes at r * 64 (16-byte piece p: dwords 0..3 of group
+ * p ^ f(r), f(r) = ((r >> 1 ^ r >> 3) & 1) | (r >> 1 & 2)) and 32 bytes at
+ * 16384 + r * 32 (8-byte slot s: dwords 4..5 of group s ^ ((r >> 3) & 3)),
+ * group g being the 32 BF6 codes of k = 128 kb + 32 g .. +31, code e at bits
+ * 6e..6e+5 of the group's 6 little-endian dwords.
+ */
+
+/* Packed int4 [rows, K/2] (the _int4/_codec.py layout) -> B6T (dst holds
+ * ceil(rows / 256) * 256 * 3K/4 bytes). */
+int cr_int4_to_bf6(const void* src, void* dst, int rows, int K, void* stream);
+
+/* cr_int4_convrot_gemm_ex on B6T operands (A6 from M rows, W6 from N rows); epilogue 0..3. */
+int cr_int4_convrot_gemm_bf6(const void* A6, const void* W6, const void* xscale, const void* wscale,
+                             const void* bias, void* out, int M, int N, int K, int epilogue, void* stream);
+
+/* cr_int4_convrot_gemm_lora on B6T operands; epilogue 0..2. */
+int cr_int4_convrot_gemm_bf6_lora(const void* A6, const void* W6, const void* xscale, const void* wscale,
+                                  const void* bias, const void* t, const void* U, int R, float scale,
+                                  void* out, int M, int N, int K, int epilogue, void* stream);
+
 /* Largest K accepted by the quantization entry points. */
 int cr_max_quant_k(void);
 

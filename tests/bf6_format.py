@@ -1,0 +1,61 @@
+"""numpy decoder of the B6T operand layout of the bf6 GEMM path (test helper).
+
+B6T of a [rows, K] matrix (K % 128 == 0): rows padded to R = ceil(rows/256)*256
+(zero codes), stored as [R/256][K/128] chunks of 24576 bytes.  In a chunk, row
+r holds 64 bytes at r*64 (16-byte piece p: dwords 0..3 of group p ^ f(r),
+f(r) = ((r>>1 ^ r>>3) & 1) | (r>>1 & 2)) and 32 bytes at 16384 + r*32 (8-byte
+slot s: dwords 4..5 of group s ^ ((r>>3) & 3)); group g = the 32 BF6 (E3M2,
+bias 3) codes of k = 128 kb + 32 g .. +31, code e at bits 6e .. 6e+5 of the
+group's 6 little-endian dwords."""
+import numpy as np
+
+CHUNK = 24576
+QOFF = 16384
+
+
+def bf6_value(code: np.ndarray) -> np.ndarray:
+    """E3M2 bias-3 codes -> float64 values (normal numbers, subnormals, zero)."""
+    code = code.astype(np.int64)
+    s = np.where(code & 0x20, -1.0, 1.0)
+    e = (code >> 2) & 7
+    m = code & 3
+    mag = np.where(e == 0, m / 4.0 * 2.0 ** -2, 2.0 ** (e - 3.0) * (1 + m / 4.0))
+    return s * mag
+
+
+def p_row_fn(r: np.ndarray) -> np.ndarray:
+    return (((r >> 1) ^ (r >> 3)) & 1) | ((r >> 1) & 2)
+
+
+def decode_b6t(b6: np.ndarray, rows: int) -> np.ndarray:
+    """uint8 B6T buffer -> int64 values [rows, K] (asserts every code is an integer
+    and every padding row is zero)."""
+    flat = np.ascontiguousarray(b6).reshape(-1)
+    R = (rows + 255) // 256 * 256
+    K = flat.size // R // 3 * 4
+    nkb = K // 128
+    ch = flat.reshape(R // 256, nkb, CHUNK)
+    r = np.arange(256)
+    P = ch[:, :, :QOFF].reshape(R // 256, nkb, 256, 4, 16)
+    Q = ch[:, :, QOFF:].reshape(R // 256, nkb, 256, 4, 8)
+    g = np.arange(4)
+    pidx = g[None, :] ^ p_row_fn(r)[:, None]                  # [256, 4] physical piece of group g
+    qidx = g[None, :] ^ ((r >> 3) & 3)[:, None]
+    Pg = P[:, :, r[:, None], pidx]                             # [T, nkb, 256, 4, 16]
+    Qg = Q[:, :, r[:, None], qidx]                             # [T, nkb, 256, 4, 8]
+    grp = np.concatenate([Pg, Qg], axis=-1)                    # [T, nkb, 256, 4, 24]
+    bits = np.unpackbits(grp, axis=-1, bitorder="little")
+    code = (bits.reshape(*grp.shape[:-1], 32, 6) * (1 << np.arange(6))).sum(-1)   # [T, nkb, 256, 4, 32]
+    vals = bf6_value(code)
+    assert np.all(vals == np.round(vals)), "non-integer bf6 code"
+    full = vals.transpose(0, 2, 1, 3, 4).reshape(R, K).astype(np.int64)
+    assert not full[rows:].any(), "padding rows must hold zero codes"
+    return full[:rows]
+
+
+def unpack_int4(packed: np.ndarray) -> np.ndarray:
+    """int8 [rows, K/2] -> int64 [rows, K] (low nibble first, two's complement)."""
+    p = packed.astype(np.int64) & 0xFF
+    lo = ((p & 15) ^ 8) - 8
+    hi = ((p >> 4) ^ 8) - 8
+    return np.stack([lo, hi], -1).reshape(packed.shape[0], -1)
