@@ -1,16 +1,18 @@
 """Benchmark of the gfx950 W4A4 ConvRot linear path.
 
 One step = the four quantized linears of a Flux-class DiT block at M = 4608
-tokens (4096 image + 512 text at 1024^2), each run as on the forward path:
-fused rotate+int4-quantize of the bf16 activation, then the W4A4 GEMM with the
-dequant + bias epilogue to bf16.
+tokens (4096 image + 512 text at 1024^2), each run as on the forward path of
+the Linear replacement: fused rotate+int4-quantize of the bf16 activation
+(written in the bf6 operand layout), then the W4A4 GEMM on the bf6 matrix
+cores (exact integer accumulation) with the dequant + bias epilogue to bf16.
+``--path int8`` times the packed-int4 / int8-MFMA kernels instead.
 
     qkv      3072 -> 9216      proj     3072 -> 3072
     mlp_up   3072 -> 12288     mlp_down 12288 -> 3072
 
 Inputs are synthetic and resident in HBM before timing: x ~ N(0,1) with 1% of
-channels x20, W ~ N(0, 0.02) in fp16 quantized once by the same kernel (load
-time, untimed), bias ~ N(0, 0.01).  Every linear has its own activation buffer
+channels x20, W ~ N(0, 0.02) in fp16 quantized once by the same kernel and
+re-encoded for the bf6 GEMM (load time, untimed), bias ~ N(0, 0.01).  Every linear has its own activation buffer
 (~450 MB live per step, beyond the 256 MB Infinity Cache).
 
 Prints one JSON line: value = effective W4A4 linear TOPS of the whole step
@@ -32,15 +34,34 @@ sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
 
 METRIC = "W4A4 linear TOPS (%int8 MFMA peak) + rotate-quant GB/s at M=4608,K=3072"
 PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA
+PEAK_FP6_TFLOPS = 10100.0    # MI355X dense fp6 / fp4 MFMA (the bf6 GEMM's instruction)
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
 M_TOKENS = 4608
 G = 256
 LINEARS = [("qkv", 3072, 9216), ("proj", 3072, 3072), ("mlp_up", 3072, 12288), ("mlp_down", 12288, 3072)]
 
 
-def rq_bytes(M, K):
-    """Algorithmic HBM bytes of one rotate+quant launch: read bf16, write nibbles + scales."""
-    return M * K * 2 + M * K // 2 + 4 * M
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "w4a4_gemm_bf6_flux_m4608_traffic.md")
+
+
+def gemm_traffic_bytes():
+    """HBM bytes per bf6 GEMM launch (mean over the four linears) as measured by
+    the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this workload, scaled
+    by the 1 GiB copy calibration; None when that summary is absent."""
+    try:
+        for line in open(TRAFFIC_SUMMARY):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def rq_bytes(M, K, path="bf6"):
+    """Algorithmic HBM bytes of one rotate+quant launch: read bf16, write the codes
+    (bf6 layout: 0.75 B per element over rows padded to 256; int4: 0.5 B) + scales."""
+    codes = ((M + 255) // 256 * 256) * K * 3 // 4 if path == "bf6" else M * K // 2
+    return M * K * 2 + codes + 4 * M
 
 
 class Linear:
@@ -51,8 +72,10 @@ class Linear:
         self.x = outlier_activations(M_TOKENS, K, seed=seed).to(dev)
         w = normal_weight(N, K, seed=seed + 1).to(dev)
         self.qw, self.ws = native.convrot_quant_int4(w, G)         # load-time weight quantization
+        self.w6 = native.int4_to_bf6(self.qw)                        # load-time bf6 operand encoding
         self.bias = normal_bias(N, seed=seed + 2).to(dev).float()
         self.qx = torch.empty((M_TOKENS, K // 2), dtype=torch.int8, device=dev)
+        self.a6 = torch.empty((native.bf6_rows(M_TOKENS), K // 4 * 3), dtype=torch.uint8, device=dev)
         self.xs = torch.empty((M_TOKENS,), dtype=torch.float32, device=dev)
         self.out = torch.empty((M_TOKENS, N), dtype=torch.bfloat16, device=dev)
         del w
@@ -68,6 +91,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time for the oracle baseline (0 disables it)")
+    ap.add_argument("--path", choices=("bf6", "int8"), default="bf6",
+                    help="GEMM path: bf6 matrix cores (the Linear's) or packed int4 on int8 MFMA")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (counter calibration)")
     args = ap.parse_args()
@@ -92,11 +117,18 @@ def main():
     vp = ctypes.c_void_p
     calls = []   # (kind, index, fn, args)
     for i, L in enumerate(lins):
-        calls.append(("rq", i, lib.ck_convrot_quant_int4,
-                      (vp(L.x.data_ptr()), 1, vp(L.qx.data_ptr()), vp(L.xs.data_ptr()), L.M, L.K, G, sptr)))
-        calls.append(("gemm", i, lib.ck_int4_convrot_gemm,
-                      (vp(L.qx.data_ptr()), vp(L.qw.data_ptr()), vp(L.xs.data_ptr()), vp(L.ws.data_ptr()),
-                       vp(L.bias.data_ptr()), vp(L.out.data_ptr()), L.M, L.N, L.K, 1, sptr)))
+        if args.path == "bf6":
+            calls.append(("rq", i, lib.cr_convrot_quant_bf6,
+                          (vp(L.x.data_ptr()), 1, vp(L.a6.data_ptr()), vp(L.xs.data_ptr()), L.M, L.K, G, sptr)))
+            calls.append(("gemm", i, lib.cr_int4_convrot_gemm_bf6,
+                          (vp(L.a6.data_ptr()), vp(L.w6.data_ptr()), vp(L.xs.data_ptr()), vp(L.ws.data_ptr()),
+                           vp(L.bias.data_ptr()), vp(L.out.data_ptr()), L.M, L.N, L.K, 1, sptr)))
+        else:
+            calls.append(("rq", i, lib.ck_convrot_quant_int4,
+                          (vp(L.x.data_ptr()), 1, vp(L.qx.data_ptr()), vp(L.xs.data_ptr()), L.M, L.K, G, sptr)))
+            calls.append(("gemm", i, lib.ck_int4_convrot_gemm,
+                          (vp(L.qx.data_ptr()), vp(L.qw.data_ptr()), vp(L.xs.data_ptr()), vp(L.ws.data_ptr()),
+                           vp(L.bias.data_ptr()), vp(L.out.data_ptr()), L.M, L.N, L.K, 1, sptr)))
 
     def step(events=None):
         for j, (_, _, fn, a) in enumerate(calls):
@@ -141,17 +173,17 @@ def main():
     gemm_ops_avg = total_ops / len(lins)
     gemm_tops = gemm_ops_avg / gemm_launch_avg / 1e12
     rq_time = sum(avg[("rq", i)] for i in range(len(lins)))
-    rq_b = sum(rq_bytes(L.M, L.K) for L in lins)
+    rq_b = sum(rq_bytes(L.M, L.K, args.path) for L in lins)
     rq_gbs = rq_b / rq_time / 1e9
     metric_rq = avg[("rq", 1)]                   # proj input: M=4608, K=3072
-    metric_rq_gbs = rq_bytes(M_TOKENS, 3072) / metric_rq / 1e9
+    metric_rq_gbs = rq_bytes(M_TOKENS, 3072, args.path) / metric_rq / 1e9
 
     detail = {}
     for i, L in enumerate(lins):
         detail[L.name] = {
             "K": L.K, "N": L.N,
             "rotate_quant_us": round(avg[("rq", i)] * 1e6, 2),
-            "rotate_quant_GBps": round(rq_bytes(L.M, L.K) / avg[("rq", i)] / 1e9, 1),
+            "rotate_quant_GBps": round(rq_bytes(L.M, L.K, args.path) / avg[("rq", i)] / 1e9, 1),
             "gemm_us": round(avg[("gemm", i)] * 1e6, 2),
             "gemm_TOPS": round(L.ops() / avg[("gemm", i)] / 1e12, 1),
         }
@@ -184,18 +216,21 @@ def main():
             "workload": "Flux-class DiT block W4A4 ConvRot linears (qkv 3072->9216, proj 3072->3072, "
                         "mlp_up 3072->12288, mlp_down 12288->3072), M=4608 tokens, bf16 in/out, G=256",
             "M": M_TOKENS, "convrot_groupsize": G, "linears": [[n, K, N] for n, K, N in LINEARS],
+            "gemm_path": args.path,
         },
         "roofline": {
-            "kernel": "w4a4_gemm_kernel<EPI_BF16>",
+            "kernel": ("w4a4_gemm_bf6_kernel<EPI_BF16> (v_mfma_scale_f32_32x32x64_f8f6f4, BF6 operands)"
+                       if args.path == "bf6" else "w4a4_gemm_pipe_kernel<EPI_BF16> (v_mfma_i32_32x32x32_i8)"),
             "bound": "mfma",
             "achieved": round(gemm_tops, 1),
-            "peak": PEAK_INT8_TOPS,
+            "peak": PEAK_FP6_TFLOPS if args.path == "bf6" else PEAK_INT8_TOPS,
             "unit": "TFLOP/s",
-            "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
-            "traffic": None,
+            "frac": round(gemm_tops / (PEAK_FP6_TFLOPS if args.path == "bf6" else PEAK_INT8_TOPS), 4),
+            "traffic": gemm_traffic_bytes() if args.path == "bf6" else None,
         },
         "rotate_quant": {
-            "kernel": "rotquant_kernel<bf16,256>",
+            "kernel": ("rotquant_wave_kernel<bf16,256,3,B6T out>" if args.path == "bf6"
+                       else "rotquant_wave_kernel<bf16,256,3,packed int4 out>"),
             "bound": "hbm",
             "GBps_at_M4608_K3072": round(metric_rq_gbs, 1),
             "frac_at_M4608_K3072": round(metric_rq_gbs / PEAK_HBM_GBS, 4),

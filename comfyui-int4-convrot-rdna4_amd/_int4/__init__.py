@@ -36,6 +36,8 @@ __all__ = [
     "pick_groupsize",
     "fuse_lora_pairs",
     "MAX_LORA_RANK",
+    "prepare_convrot_w4a4_weight_bf6",
+    "bf6_path_ok",
 ]
 
 # largest concatenated rank of the fused LoRA side path (padded to a multiple of 32)
@@ -150,6 +152,22 @@ def dequantize_convrot_w4a4_weight(
     return torch.matmul(w.reshape(N, K // G, G), h.T).reshape(N, K).to(output_dtype)
 
 
+def bf6_path_ok(in_features: int) -> bool:
+    """True when a linear of this input width runs on the bf6 matrix-core GEMM
+    (K % 128 == 0 and the fused quantizer covers K); others use the int8 GEMM."""
+    return in_features % 128 == 0 and in_features <= native.max_quant_bf6_k()
+
+
+def prepare_convrot_w4a4_weight_bf6(qweight: torch.Tensor) -> torch.Tensor | None:
+    """Load-time re-encoding of a packed int4 weight [N, K/2] into the B6T bf6
+    operand layout of the fast GEMM (uint8 [ceil(N/256)*256, 3K/4], the same
+    integer codes).  Returns None when the weight's K cannot use that path."""
+    K = qweight.shape[-1] * 2
+    if not bf6_path_ok(K):
+        return None
+    return native.int4_to_bf6(_on_gpu(qweight).contiguous())
+
+
 def convrot_w4a4_linear(
     x: torch.Tensor,
     qweight: torch.Tensor,
@@ -160,6 +178,7 @@ def convrot_w4a4_linear(
     linear_dtype: str = "int4",
     *,
     lora: tuple[torch.Tensor, torch.Tensor] | None = None,
+    qweight_bf6: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Compute ``x @ W.T + bias`` with the gfx950 W4A4 ConvRot path
     (reference _int4/__init__.py:94-138).
@@ -168,6 +187,14 @@ def convrot_w4a4_linear(
     ``(x @ D.T) @ U.T`` inside the GEMM epilogue (one extra kernel for the
     down projection), the fused form of the per-adapter side path of the
     reference's Linear (int4_ops.py:181-192).
+
+    ``qweight_bf6`` (from :func:`prepare_convrot_w4a4_weight_bf6`, made once
+    at load time) selects the bf6 matrix-core GEMM: the activation is
+    quantized straight into the bf6 operand layout and the integer products
+    run on v_mfma_scale_f32_32x32x64_f8f6f4, whose fp32 accumulation of these
+    small integers is exact, so the output is bit-identical to the int8-MFMA
+    GEMM's.  Without it, inputs whose K allows it still take the bf6 GEMM with
+    the weight re-encoded on the fly.
 
     Two kernels per call, both on torch's current stream: the fused
     rotate+quantize of x, then the W4A4 GEMM with the dequant epilogue.  Every
@@ -190,19 +217,31 @@ def convrot_w4a4_linear(
     x2d = x.reshape(-1, orig_shape[-1]).contiguous()
     if x2d.dtype not in native._IN_DTYPE_CODE:
         x2d = x2d.to(torch.float32)
-    qact, x_scale = native.convrot_quant_int4(x2d, convrot_groupsize)
     out_dtype = x.dtype if x.dtype in _NATIVE_OUT else torch.float32
-    if lora is None:
-        out = native.int4_convrot_gemm(qact, qweight, x_scale, wscales, bias, out_dtype)
-    else:
+    epi = native.EPI_BF16 if out_dtype == torch.bfloat16 else native.EPI_F32
+    K, N = x2d.shape[1], qweight.shape[0]
+    t = up = None
+    if lora is not None:
         down, up = lora
-        if down.shape[1] != x2d.shape[1] or up.shape[0] != qweight.shape[0] or up.shape[1] != down.shape[0]:
-            raise ValueError(f"LoRA shapes D {tuple(down.shape)} U {tuple(up.shape)} do not fit "
-                             f"K={x2d.shape[1]} N={qweight.shape[0]}")
+        if down.shape[1] != K or up.shape[0] != N or up.shape[1] != down.shape[0]:
+            raise ValueError(f"LoRA shapes D {tuple(down.shape)} U {tuple(up.shape)} do not fit K={K} N={N}")
         xd = x2d if x2d.dtype in (torch.bfloat16, torch.float16) else x2d.to(torch.bfloat16)
         t = native.lora_down(xd, down)
-        epi = native.EPI_BF16 if out_dtype == torch.bfloat16 else native.EPI_F32
-        out = native.int4_convrot_gemm_lora(qact, qweight, x_scale, wscales, bias, t, up, 1.0, epi)
+    if bf6_path_ok(K):
+        w6 = qweight_bf6 if qweight_bf6 is not None else prepare_convrot_w4a4_weight_bf6(qweight)
+        if w6.shape != (native.bf6_rows(N), K // 4 * 3):
+            raise ValueError(f"qweight_bf6 of shape {tuple(w6.shape)} does not encode a [{N}, {K}] weight")
+        a6, x_scale = native.convrot_quant_bf6(x2d, convrot_groupsize)
+        if t is None:
+            out = native.int4_convrot_gemm_bf6(a6, w6, x_scale, wscales, bias, epi)
+        else:
+            out = native.int4_convrot_gemm_bf6_lora(a6, w6, x_scale, wscales, bias, t, up, 1.0, epi)
+    else:
+        qact, x_scale = native.convrot_quant_int4(x2d, convrot_groupsize)
+        if t is None:
+            out = native.int4_convrot_gemm(qact, qweight, x_scale, wscales, bias, out_dtype)
+        else:
+            out = native.int4_convrot_gemm_lora(qact, qweight, x_scale, wscales, bias, t, up, 1.0, epi)
     if out.dtype != x.dtype:
         out = out.to(x.dtype)
     return out.reshape(*orig_shape[:-1], qweight.shape[0])

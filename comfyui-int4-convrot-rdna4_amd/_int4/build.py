@@ -15,7 +15,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _PKG = os.path.dirname(_HERE)
 _CSRC = os.path.join(_PKG, "csrc")
 SOURCES = ("rotquant.hip", "gemm.hip", "gemm_bf6.hip", "lora.hip", "capi.hip")
-HEADERS = ("common.h", "gemm_common.h")
+HEADERS = ("common.h", "gemm_common.h", "b6t_layout.h")
 ARCH = "gfx950"
 
 

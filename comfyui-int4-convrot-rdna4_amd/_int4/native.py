@@ -37,6 +37,8 @@ _SIGNATURES = {
     "cr_lora_down": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
     "cr_int4_convrot_gemm_lora": ([_vp] * 7 + [_i, ctypes.c_float, _vp] + [_i] * 4 + [_vp], _i),
     "cr_int4_to_bf6": ([_vp, _vp, _i, _i, _vp], _i),
+    "cr_convrot_quant_bf6": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
+    "cr_max_quant_bf6_k": ([], _i),
     "cr_int4_convrot_gemm_bf6": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
     "cr_int4_convrot_gemm_bf6_lora": ([_vp] * 7 + [_i, ctypes.c_float, _vp] + [_i] * 4 + [_vp], _i),
     "cr_max_quant_k": ([], _i),
@@ -283,6 +285,31 @@ def int4_to_bf6(packed: torch.Tensor) -> torch.Tensor:
     if rc != 0:
         raise RuntimeError(f"cr_int4_to_bf6 failed, hipError={rc}")
     return out
+
+
+def max_quant_bf6_k() -> int:
+    return load_library().cr_max_quant_bf6_k()
+
+
+def convrot_quant_bf6(x: torch.Tensor, convrot_groupsize: int):
+    """Fused rotate + int4 quantize of x [M, K] (f32/bf16/f16) straight into the
+    B6T bf6 operand layout.  Returns (a6 uint8 [bf6_rows(M), 3K/4], scale f32 [M]);
+    the codes and scales equal convrot_quant_int4's.  K % 128 == 0, K <= max_quant_bf6_k()."""
+    lib = load_library()
+    _check_cuda(x)
+    if x.dim() != 2 or x.dtype not in _IN_DTYPE_CODE:
+        raise ValueError("x must be a 2-D f32/bf16/f16 tensor")
+    x = _aligned(x)
+    M, K = x.shape
+    if K % 128 != 0 or K > lib.cr_max_quant_bf6_k() or K % convrot_groupsize != 0:
+        raise ValueError(f"bf6 activation quantization needs K % 128 == 0 and K <= {lib.cr_max_quant_bf6_k()}")
+    a6 = torch.empty((bf6_rows(M), K // 4 * 3), dtype=torch.uint8, device=x.device)
+    s = torch.empty((M,), dtype=torch.float32, device=x.device)
+    rc = lib.cr_convrot_quant_bf6(_ptr(x), _IN_DTYPE_CODE[x.dtype], _ptr(a6), _ptr(s), M, K, convrot_groupsize,
+                                  _stream(x.device))
+    if rc != 0:
+        raise RuntimeError(f"cr_convrot_quant_bf6 failed, hipError={rc}")
+    return a6, s
 
 
 def _bf6_gemm_args(a6, w6, x_scale, w_scale, bias, M, N):

@@ -1,0 +1,90 @@
+// The B6T operand layout of the bf6 GEMM path (shared by the producers in
+// rotquant.hip / gemm_bf6.hip and the GEMM consumer).
+//
+// A matrix [rows, K] with K % 128 == 0 is stored with rows padded to a
+// multiple of 256 (zero codes) as [rows/256][K/128] chunks of 24576 bytes;
+// the chunk of (row tile, 128-k block) is one operand half of a GEMM LDS
+// stage, so the GEMM copies it with contiguous 1 KB DMA instructions:
+//   bytes     0..16383  P part: row r at r*64, 16-byte piece p holds dwords
+//                       0..3 of group p ^ f(r) (f: swz below)
+//   bytes 16384..24575  Q part: row r at 16384 + r*32, 8-byte slot s holds
+//                       dwords 4..5 of group s ^ ((r >> 3) & 3)
+// Group g is the MFMA operand of k = 128 kb + 32 g .. +31: 32 BF6 (E3M2,
+// exponent bias 3) codes, code e in bits 6e .. 6e+5 of the 6-dword
+// little-endian bit stream (lane l of v_mfma_*_f8f6f4 supplies row l % 32,
+// k half l / 32).  Both permutations make the GEMM's fragment reads
+// bank-conflict-free.
+#pragma once
+
+#include "common.h"
+
+namespace convrot {
+
+constexpr int B6_CHUNK = 24576;          // bytes of one (256-row tile, 128-k block) chunk
+constexpr int B6_QOFF = 16384;           // Q part offset inside a chunk
+
+#ifndef CONVROT_SWZ64
+#define CONVROT_SWZ64 1
+#endif
+// chunk swizzle: row r stores its logical chunk c at physical chunk c ^ f(r).
+// With 64-byte rows a 16-byte read of chunk c by rows r..r+15 is conflict-free
+// when (r & 3, f(r)) takes 16 distinct values (64 banks x 4 B, 16 lanes per
+// phase) and when (r & 1, f(r)) takes 8 distinct values over r..r+7 (32 banks,
+// 8 lanes per phase); f = (bit1 ^ bit3) | bit2 << 1 satisfies both.
+__host__ __device__ __forceinline__ int swz(int row, int chunk) {
+    if (CONVROT_SWZ64) return chunk ^ ((((row >> 1) ^ (row >> 3)) & 1) | ((row >> 1) & 2));
+    return chunk ^ ((row >> 1) & 3);
+}
+
+// byte offsets of group g's P and Q pieces for row r (0..255) inside a chunk
+__host__ __device__ __forceinline__ int b6_p_off(int r, int g) { return r * 64 + swz(r, g) * 16; }
+__host__ __device__ __forceinline__ int b6_q_off(int r, int g) { return B6_QOFF + r * 32 + 8 * (g ^ ((r >> 3) & 3)); }
+
+// BF6 code of an integer -8..7: 0 -> 0, |q| = 2^e (1 + m/4) -> (e + 3) << 2 | m, sign 0x20.
+constexpr uint32_t bf6_code_of_int(int q) {
+    if (q == 0) return 0;
+    const int a = q < 0 ? -q : q;
+    int e = 0;
+    while ((a >> (e + 1)) != 0) ++e;
+    const int m = ((a << 2) >> e) & 3;
+    return (q < 0 ? 0x20u : 0u) | (uint32_t)((e + 3) << 2) | (uint32_t)m;
+}
+static_assert(bf6_code_of_int(7) == 23 && bf6_code_of_int(-8) == 56 && bf6_code_of_int(3) == 18, "bf6");
+
+// codes of the int4 values whose two's complement nibbles are base .. base+3,
+// one per byte (the byte lookup table of bf6_bytes)
+constexpr uint32_t bf6_lut4(int base) {
+    uint32_t t = 0;
+    for (int i = 0; i < 4; ++i) {
+        const int n = base + i;
+        t |= bf6_code_of_int(n >= 8 ? n - 16 : n) << (8 * i);
+    }
+    return t;
+}
+
+// Four bytes whose low nibbles are int4 codes (two's complement) -> their
+// four BF6 codes, one per byte: two v_perm_b32 byte lookups (nibbles 0..7 and
+// 8..15; selector values 0..3 take bytes of the second source, 4..7 of the
+// first) and a per-byte select on nibble bit 3.
+__device__ __forceinline__ uint32_t bf6_bytes(uint32_t w) {
+    const uint32_t sel = w & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(bf6_lut4(4), bf6_lut4(0), sel);
+    const uint32_t hi = __builtin_amdgcn_perm(bf6_lut4(12), bf6_lut4(8), sel);
+    const uint32_t neg = ((w >> 3) & 0x01010101u) * 0xFFu;       // 0xFF in bytes with nibble bit 3
+    return (hi & neg) | (lo & ~neg);
+}
+
+// 16 BF6 codes (one per byte, 4 per dword) -> 96 packed bits (code e at 6e)
+__device__ __forceinline__ void bf6_pack16(const uint32_t (&c)[4], uint32_t (&d)[3]) {
+    uint32_t f[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t w = c[k];
+        f[k] = (w & 0x3Fu) | ((w >> 2) & 0xFC0u) | ((w >> 4) & 0x3F000u) | ((w >> 6) & 0xFC0000u);
+    }
+    d[0] = f[0] | (f[1] << 24);
+    d[1] = (f[1] >> 8) | (f[2] << 16);
+    d[2] = (f[2] >> 16) | (f[3] << 8);
+}
+
+}  // namespace convrot

@@ -16,6 +16,9 @@ hipError_t gemm_lora_launch(const int8_t* Xp, const int8_t* Wp, const float* xs,
 hipError_t lora_down_launch(const void* x, int in_dtype, const void* D, void* t, int M, int K, int R,
                             hipStream_t st);
 hipError_t int4_to_bf6_launch(const void* src, void* dst, int rows, int K, hipStream_t st);
+hipError_t rotquant_b6_launch(const void* x, int in_dtype, uint8_t* a6, float* s, int M, int K, int G,
+                              hipStream_t st);
+int rotquant_b6_max_k();
 hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, const float* ws, const float* bias,
                            const void* t, const void* U, int R, float scale, void* out, int M, int N, int K,
                            int epi, hipStream_t st);
@@ -95,6 +98,16 @@ API int cr_int4_to_bf6(const void* src, void* dst, int rows, int K, void* stream
     if (rows < 0 || !bf6_k_ok(K)) return -1;
     return (int)convrot::int4_to_bf6_launch(src, dst, rows, K, reinterpret_cast<hipStream_t>(stream));
 }
+
+API int cr_convrot_quant_bf6(const void* x, int in_dtype, void* a6out, void* scaleout, int M, int K, int G,
+                             void* stream) {
+    if (!quant_args_ok(in_dtype, M, K, G) || K % 128 != 0 || K > convrot::rotquant_b6_max_k()) return -1;
+    return (int)convrot::rotquant_b6_launch(x, in_dtype, reinterpret_cast<uint8_t*>(a6out),
+                                            reinterpret_cast<float*>(scaleout), M, K, G,
+                                            reinterpret_cast<hipStream_t>(stream));
+}
+
+API int cr_max_quant_bf6_k(void) { return convrot::rotquant_b6_max_k(); }
 
 API int cr_int4_convrot_gemm_bf6(const void* A6, const void* W6, const void* xscale, const void* wscale,
                                  const void* bias, void* out, int M, int N, int K, int epilogue, void* stream) {

@@ -171,7 +171,7 @@ template <int EPI, int WN, bool LORA>
 __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
         const int8_t* __restrict__ Xp, const int8_t* __restrict__ Wp,
         const float* __restrict__ xs, const float* __restrict__ ws, const float* __restrict__ bias,
-        void* __restrict__ out, int M, int N, int K, LoraArgs lora) {
+        void* __restrict__ out, int M, int N, int K, LoraArgs lora, int gm) {
     extern __shared__ __attribute__((aligned(16))) uint8_t plds[];
 
     constexpr int P_THREADS = 128 * WN;                 // 2 x WN waves
@@ -182,16 +182,10 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
-    const int tiles_m = (M + P_BM - 1) / P_BM;
-    const int ntiles = tiles_m * ((N + P_BN - 1) / P_BN);
-    // XCD-aware renumbering: workgroup b runs on XCD b % 8
-    int b = blockIdx.x;
-    {
-        const int per = ntiles / 8, rem = ntiles % 8, x = b % 8, l = b / 8;
-        b = x * per + min(x, rem) + l;
-    }
-    const int m0 = (b % tiles_m) * P_BM;
-    const int n0 = (b / tiles_m) * P_BN;
+    int tm, tn;
+    tile_of_block(blockIdx.x, (M + P_BM - 1) / P_BM, (N + P_BN - 1) / P_BN, gm, tm, tn);
+    const int m0 = tm * P_BM;
+    const int n0 = tn * P_BN;
     const int Kb = K / 2;
     const int nkb = K / P_BK;
     float* sc = reinterpret_cast<float*>(plds + P_STAGES * P_STAGE_BYTES);
@@ -299,7 +293,8 @@ static hipError_t launch_epi(const int8_t* Xp, const int8_t* Wp, const float* xs
             attr_set[dev] = true;
         }
         hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<EPI, WN, LORA>), dim3(ntiles), dim3(128 * WN),
-                           P_LDS_BYTES, st, Xp, Wp, xs, ws, bias, out, M, N, K, la);
+                           P_LDS_BYTES, st, Xp, Wp, xs, ws, bias, out, M, N, K, la,
+                           tile_group_rows((M + P_BM - 1) / P_BM));
     } else {
         dim3 grid((N + TBN - 1) / TBN, (M + TBM - 1) / TBM), block(NTHR);
         hipLaunchKernelGGL((w4a4_gemm_kernel<EPI, LORA>), grid, block, 0, st, Xp, Wp, xs, ws, bias, out, M, N, K, la);

@@ -10,20 +10,9 @@
 // (gemm_common.h).  With unit block scales (E8M0 127) the scale operands are
 // exact multiplications by 1.
 //
-// Operand format ("B6T", produced by int4_to_bf6t_kernel from the packed int4
-// layout, or directly by the fused rotate+quant kernel): a matrix [rows, K]
-// with K % 128 == 0, rows padded to a multiple of 256 (padding rows hold
-// zero codes), stored tile-major as [rows/256][K/128] chunks of 24576 bytes.
-// The chunk of (row tile, 128-k block) is exactly one operand half of an LDS
-// pipeline stage, so the GEMM copies it with 1 KB contiguous DMA instructions:
-//   bytes     0..16383  P part: row r at r*64, 16-byte chunk p holds dwords 0..3
-//                       of group p ^ f(r) (f: the swz() row function)
-//   bytes 16384..24575  Q part: row r at 16384 + r*32, 8-byte slot s holds
-//                       dwords 4..5 of group s ^ ((r >> 3) & 3)
-// where group g is the MFMA operand of k = 128 kb + 32 g .. +31: 32 BF6 codes,
-// code e in bits 6e .. 6e+5 of the 6-dword little-endian bit stream (the
-// operand layout of the instruction: lane l supplies row l % 32, k half l / 32).
-// Both permutations make the fragment reads bank-conflict-free.
+// Operands are in the B6T layout (b6t_layout.h), produced by
+// int4_to_bf6t_kernel from the packed int4 layout or directly by the fused
+// rotate+quant kernel (rotquant.hip).
 
 #include "gemm_common.h"
 
@@ -32,15 +21,6 @@ namespace convrot {
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-// BF6 code of an integer -8..7: 0 -> 0, |q| = 2^e (1 + m/4) -> (e + 3) << 2 | m, sign 0x20.
-constexpr uint32_t bf6_code_of_int(int q) {
-    if (q == 0) return 0;
-    const int a = q < 0 ? -q : q;
-    int e = 0;
-    while ((a >> (e + 1)) != 0) ++e;
-    const int m = ((a << 2) >> e) & 3;
-    return (q < 0 ? 0x20u : 0u) | (uint32_t)((e + 3) << 2) | (uint32_t)m;
-}
 // codes of nibbles base .. base+7 (two's complement int4), 6 bits each
 constexpr uint64_t bf6_nibble_table(int base) {
     uint64_t t = 0;
@@ -50,7 +30,6 @@ constexpr uint64_t bf6_nibble_table(int base) {
     }
     return t;
 }
-static_assert(bf6_code_of_int(7) == 23 && bf6_code_of_int(-8) == 56 && bf6_code_of_int(3) == 18, "bf6");
 
 __device__ __forceinline__ uint32_t bf6_of_nibble(uint32_t n) {
     constexpr uint64_t LO = bf6_nibble_table(0), HI = bf6_nibble_table(8);
@@ -72,9 +51,6 @@ __device__ __forceinline__ void encode_group(uint4 p, uint32_t (&d)[6]) {
         if ((bit & 31) > 26) d[(bit >> 5) + 1] |= code >> (32 - (bit & 31));
     }
 }
-
-constexpr int B6_CHUNK = 24576;          // bytes of one (256-row tile, 128-k block) chunk
-constexpr int B6_QOFF = 16384;           // Q part offset inside a chunk
 
 // packed int4 [rows, K/2] -> B6T; one thread per (row, 128-k block) of the
 // padded matrix, consecutive threads on consecutive rows of one chunk.
@@ -99,8 +75,8 @@ __global__ __launch_bounds__(256) void int4_to_bf6t_kernel(const uint8_t* __rest
     for (int g = 0; g < 4; ++g) {
         uint32_t c[6];
         encode_group(in[g], c);
-        *reinterpret_cast<uint4*>(d + r * 64 + swz(r, g) * 16) = make_uint4(c[0], c[1], c[2], c[3]);
-        *reinterpret_cast<uint2*>(d + B6_QOFF + r * 32 + 8 * (g ^ ((r >> 3) & 3))) = make_uint2(c[4], c[5]);
+        *reinterpret_cast<uint4*>(d + b6_p_off(r, g)) = make_uint4(c[0], c[1], c[2], c[3]);
+        *reinterpret_cast<uint2*>(d + b6_q_off(r, g)) = make_uint2(c[4], c[5]);
     }
 }
 
@@ -131,23 +107,17 @@ template <int EPI, bool LORA>
 __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
         const uint8_t* __restrict__ A6, const uint8_t* __restrict__ W6,
         const float* __restrict__ xs, const float* __restrict__ ws, const float* __restrict__ bias,
-        void* __restrict__ out, int M, int N, int K, LoraArgs lora) {
+        void* __restrict__ out, int M, int N, int K, LoraArgs lora, int gm) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds6[];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave >> 2, wn = wave & 3;
-    const int tiles_m = (M + B6_BM - 1) / B6_BM;
-    const int ntiles = tiles_m * ((N + B6_BN - 1) / B6_BN);
-    // XCD-aware renumbering: workgroup b runs on XCD b % 8
-    int b = blockIdx.x;
-    {
-        const int per = ntiles / 8, rem = ntiles % 8, x = b % 8, l = b / 8;
-        b = x * per + min(x, rem) + l;
-    }
-    const int m0 = (b % tiles_m) * B6_BM;
-    const int n0 = (b / tiles_m) * B6_BN;
+    int tm, tn;
+    tile_of_block(blockIdx.x, (M + B6_BM - 1) / B6_BM, (N + B6_BN - 1) / B6_BN, gm, tm, tn);
+    const int m0 = tm * B6_BM;
+    const int n0 = tn * B6_BN;
     const int nkb = K / 128;
 
     float* sc = reinterpret_cast<float*>(lds6 + B6_RING_BYTES);
@@ -184,10 +154,10 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
             const int g = 2 * s2 + fhalf;
-            offPa[s2] = ra * 64 + swz(ra, g) * 16;
-            offQa[s2] = B6_QOFF + ra * 32 + 8 * (g ^ ((ra >> 3) & 3));
-            offPb[s2] = B6_CHUNK + rb * 64 + swz(rb, g) * 16;
-            offQb[s2] = B6_CHUNK + B6_QOFF + rb * 32 + 8 * (g ^ ((rb >> 3) & 3));
+            offPa[s2] = b6_p_off(ra, g);
+            offQa[s2] = b6_q_off(ra, g);
+            offPb[s2] = B6_CHUNK + b6_p_off(rb, g);
+            offQb[s2] = B6_CHUNK + b6_q_off(rb, g);
         }
     }
     // one 128-k block from the stage the offsets currently point into: all 12
@@ -266,7 +236,7 @@ static hipError_t launch_bf6(const uint8_t* A6, const uint8_t* W6, const float* 
     }
     const int ntiles = ((M + B6_BM - 1) / B6_BM) * ((N + B6_BN - 1) / B6_BN);
     hipLaunchKernelGGL((w4a4_gemm_bf6_kernel<EPI, LORA>), dim3(ntiles), dim3(B6_THREADS), B6_LDS_BYTES, st,
-                       A6, W6, xs, ws, bias, out, M, N, K, la);
+                       A6, W6, xs, ws, bias, out, M, N, K, la, tile_group_rows((M + B6_BM - 1) / B6_BM));
     return hipGetLastError();
 }
 

@@ -4,6 +4,7 @@
 // global->LDS DMA issue and the pipeline waits.
 #pragma once
 
+#include "b6t_layout.h"
 #include "common.h"
 
 namespace convrot {
@@ -232,23 +233,35 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
     }
 }
 
-#ifndef CONVROT_SWZ64
-#define CONVROT_SWZ64 1
-#endif
-// chunk swizzle: row r stores its logical chunk c at physical chunk c ^ f(r).
-// With 64-byte rows a 16-byte read of chunk c by rows r..r+15 is conflict-free
-// when (r & 3, f(r)) takes 16 distinct values (64 banks x 4 B, 16 lanes per
-// phase) and when (r & 1, f(r)) takes 8 distinct values over r..r+7 (32 banks,
-// 8 lanes per phase); f = (bit1 ^ bit3) | bit2 << 1 satisfies both.
-__device__ __forceinline__ int swz(int row, int chunk) {
-    if (CONVROT_SWZ64) return chunk ^ ((((row >> 1) ^ (row >> 3)) & 1) | ((row >> 1) & 2));
-    return chunk ^ ((row >> 1) & 3);
-}
-
 // s_waitcnt immediate that waits until at most n vector-memory operations are
 // outstanding (vmcnt split over bits 3:0 and 15:14; expcnt / lgkmcnt not waited)
 constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
+
+// Tile of workgroup `bid` in a tiles_m x tiles_n grid: workgroups are
+// renumbered so that each XCD (bid % 8 on MI355X's round-robin dispatch) gets a
+// contiguous range of tiles, and tiles are ordered m-fastest within groups of
+// `gm` tile rows, so the tiles an XCD runs at one time form a compact block
+// that shares A and B chunks in its L2.
+__device__ __forceinline__ void tile_of_block(int bid, int tiles_m, int tiles_n, int gm, int& tm, int& tn) {
+    const int ntiles = tiles_m * tiles_n;
+    const int per = ntiles / 8, rem = ntiles % 8, x = bid % 8, l = bid / 8;
+    const int b = x * per + min(x, rem) + l;
+    const int grp = b / (gm * tiles_n), inb = b % (gm * tiles_n);
+    const int rows_in = min(gm, tiles_m - grp * gm);
+    tm = grp * gm + inb % rows_in;
+    tn = inb / rows_in;
+}
+
+// Row-group size for tile_of_block: about 8 tile rows, a divisor of tiles_m
+// when one is close (18 row tiles -> 9).
+inline int tile_group_rows(int tiles_m) {
+    if (tiles_m <= 8) return tiles_m > 0 ? tiles_m : 1;
+    const int cand[] = {8, 9, 7, 6, 10, 12};
+    for (int c : cand)
+        if (tiles_m % c == 0) return c;
+    return 8;
+}
 
 // One 16-byte-per-lane global->LDS DMA (global_load_lds_dwordx4): lane i of
 // the wave writes lds_addr + 16 i.  Issued from inline asm so the compiler

@@ -37,6 +37,7 @@
 //   f16:  P = fl32(fl64(xr * fl64(1/s))), error <= 2^-24 + 2^-52 < 2^-23.
 // f32 uses the IEEE fp32 division directly.
 
+#include "b6t_layout.h"
 #include "common.h"
 
 namespace convrot {
@@ -348,7 +349,26 @@ __device__ __forceinline__ float jam_to_f32(double d) {
 }
 
 
-template <int DT, int G, int NPMAX>
+// Store the 16 codes of elements k0 .. k0+15 of `row` (3 packed dwords, k0 % 16
+// == 0) at their place in a B6T buffer: the first half of an MFMA group goes to
+// dwords 0..2 of its P piece, the second half to dword 3 and the Q piece.
+__device__ __forceinline__ void b6_store_half(int8_t* out, int row, int K, int k0, const uint32_t (&d)[3]) {
+    const int kb = k0 >> 7, g = (k0 >> 5) & 3, r = row & 255;
+    uint8_t* chunk = reinterpret_cast<uint8_t*>(out) + ((size_t)(row >> 8) * (K >> 7) + kb) * B6_CHUNK;
+    if (((k0 >> 4) & 1) == 0) {
+        uint32_t* p = reinterpret_cast<uint32_t*>(chunk + b6_p_off(r, g));
+        p[0] = d[0];
+        p[1] = d[1];
+        p[2] = d[2];
+    } else {
+        reinterpret_cast<uint32_t*>(chunk + b6_p_off(r, g))[3] = d[0];
+        *reinterpret_cast<uint2*>(chunk + b6_q_off(r, g)) = make_uint2(d[1], d[2]);
+    }
+}
+
+// B6: write the codes in the B6T layout of the bf6 GEMM (b6t_layout.h) instead
+// of packed nibbles (K % 128 == 0; rows M .. ceil(M/256)*256 get zero codes).
+template <int DT, int G, int NPMAX, bool B6>
 __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
         const void* __restrict__ x, int8_t* __restrict__ qout, float* __restrict__ sout, int M, int K) {
     constexpr int LPG = G / kChunk;
@@ -474,7 +494,14 @@ __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
                 wave_sync();
                 const uint4 w = reinterpret_cast<const uint4*>(cb)[lane];
                 wave_sync();
-                if (ok) {
+                if (B6 && ok) {
+                    // lane pair (2g', 2g'+1) holds the 32 codes of one MFMA group: the even
+                    // lane its dwords 0..2, the odd lane dwords 3..5
+                    const uint32_t c4[4] = {bf6_bytes(w.x), bf6_bytes(w.y), bf6_bytes(w.z), bf6_bytes(w.w)};
+                    uint32_t d[3];
+                    bf6_pack16(c4, d);
+                    b6_store_half(qout, row, K, c * kChunk, d);
+                } else if (ok) {
                     const uint32_t ws[4] = {w.x & 0x0f0f0f0fu, w.y & 0x0f0f0f0fu, w.z & 0x0f0f0f0fu,
                                             w.w & 0x0f0f0f0fu};
                     uint32_t o[2];
@@ -489,6 +516,12 @@ __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
                 }
             }
         }
+    }
+    if constexpr (B6) {   // zero codes in the padding rows of the last 256-row tile
+        const int mpad = (M + 255) & ~255;
+        const uint32_t z[3] = {0u, 0u, 0u};
+        for (int prow = M + blockIdx.x * kWaves + wv; prow < mpad; prow += nwaves)
+            for (int c = lane; c < nchunks; c += 64) b6_store_half(qout, prow, K, c * kChunk, z);
     }
 }
 
@@ -506,20 +539,21 @@ static int num_cus() {
     return g_num_cus;
 }
 
-template <int DT, int G>
+template <int DT, int G, bool B6>
 static hipError_t rq_wave_launch(const void* x, int8_t* q, float* s, int M, int K, hipStream_t st) {
     const int np = (K / kChunk + 63) / 64;
     // enough waves to keep every CU busy; each wave then walks rows persistently
     const int max_wg = num_cus() * 8;
     int grid = (M + kWaves - 1) / kWaves;
     if (grid > max_wg) grid = max_wg;
+    if (grid < 1) grid = 1;
     dim3 g(grid), b(64 * kWaves);
     if (np <= 3)
-        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 3>), g, b, 0, st, x, q, s, M, K);
+        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 3, B6>), g, b, 0, st, x, q, s, M, K);
     else if (np <= 6)
-        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 6>), g, b, 0, st, x, q, s, M, K);
+        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 6, B6>), g, b, 0, st, x, q, s, M, K);
     else
-        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 12>), g, b, 0, st, x, q, s, M, K);
+        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 12, B6>), g, b, 0, st, x, q, s, M, K);
     return hipGetLastError();
 }
 
@@ -552,7 +586,7 @@ template <int DT, int G, bool STOCH>
 static hipError_t rq_launch_g(const void* x, const void* noise, int8_t* q, float* s, int M, int K,
                               hipStream_t st) {
     if (M == 0) return hipSuccess;
-    if (!STOCH && K <= kWaveMaxK) return rq_wave_launch<DT, G>(x, q, s, M, K, st);
+    if (!STOCH && K <= kWaveMaxK) return rq_wave_launch<DT, G, false>(x, q, s, M, K, st);
     RQPlan pl;
     if (rq_plan(M, K, G, &pl) != 0) return hipErrorInvalidValue;
     dim3 grid(pl.grid), block(pl.block);
@@ -595,5 +629,28 @@ hipError_t rotquant_launch(const void* x, int in_dtype, const void* noise, int8_
 }
 
 int rotquant_max_k() { return 8 * kMaxThreads * kChunk; }
+
+// fused rotate + quantize into the B6T layout (K % 128 == 0, K <= 12288)
+hipError_t rotquant_b6_launch(const void* x, int in_dtype, uint8_t* a6, float* s, int M, int K, int G,
+                              hipStream_t st) {
+    if (K % 128 != 0 || K > kWaveMaxK || M < 0) return hipErrorInvalidValue;
+    int8_t* q = reinterpret_cast<int8_t*>(a6);
+#define RB6_G(DT)                                                                                   \
+    switch (G) {                                                                                    \
+        case 16: return rq_wave_launch<DT, 16, true>(x, q, s, M, K, st);                            \
+        case 64: return rq_wave_launch<DT, 64, true>(x, q, s, M, K, st);                            \
+        case 256: return rq_wave_launch<DT, 256, true>(x, q, s, M, K, st);                          \
+        default: return hipErrorInvalidValue;                                                       \
+    }
+    switch (in_dtype) {
+        case DT_F32: RB6_G(DT_F32)
+        case DT_BF16: RB6_G(DT_BF16)
+        case DT_F16: RB6_G(DT_F16)
+        default: return hipErrorInvalidValue;
+    }
+#undef RB6_G
+}
+
+int rotquant_b6_max_k() { return kWaveMaxK; }
 
 }  // namespace convrot

@@ -141,6 +141,7 @@ if _COMFY_OPS and _CK_OK:
                 self._qs = None       # per-row scale f32 [N]
                 self._qgs = None      # convrot groupsize
                 self._qmode = None    # "int4" | "int8" | None (bf16)
+                self._q6 = None       # int4 weight re-encoded for the bf6 matrix-core GEMM (load time)
                 self._dyn_lora = None
                 self._dyn_fused = None   # (D, U) bf16: plain LoRAs fused into the GEMM epilogue
                 self._dyn_rest = None    # adapters that keep the generic h() side path
@@ -302,6 +303,7 @@ if _COMFY_OPS and _CK_OK:
                 self._q = w.to(dev).contiguous()
                 self._qs = state_dict[skey].to(dev, torch.float32).reshape(-1).contiguous()
                 self._qgs, self._qmode = gs, mode
+                self._q6 = _ck.prepare_convrot_w4a4_weight_bf6(self._q) if mode == "int4" else None
                 self.weight = None
                 for k in (wkey, skey, qkey):
                     state_dict.pop(k, None)
@@ -361,6 +363,7 @@ if _COMFY_OPS and _CK_OK:
                         qw, ws = _ck.quantize_convrot_w4a4_weight(
                             w.to(dev, torch.float16), convrot_groupsize=gs, stochastic_rounding=stoch)
                         self._q, self._qs, self._qgs, self._qmode = qw, ws.float(), gs, mode
+                        self._q6 = _ck.prepare_convrot_w4a4_weight_bf6(qw)
                         self.weight = None
                         state_dict.pop(wkey, None)
                         self._take_bias(state_dict, prefix, dev)
@@ -378,6 +381,8 @@ if _COMFY_OPS and _CK_OK:
                 if self._q.device != x.device:
                     self._q = self._q.to(x.device)
                     self._qs = self._qs.to(x.device)
+                    if self._q6 is not None:
+                        self._q6 = self._q6.to(x.device)
                 bias = self.bias
                 if bias is not None and bias.device != x.device:
                     bias = bias.to(x.device)
@@ -388,8 +393,8 @@ if _COMFY_OPS and _CK_OK:
                 fused = self._dyn_fused
                 if fused is not None and fused[0].device != x.device:
                     fused = self._dyn_fused = (fused[0].to(x.device), fused[1].to(x.device))
-                out = _ck.convrot_w4a4_linear(x, self._q, self._qs, bias=bias,
-                                              convrot_groupsize=self._qgs, lora=fused)
+                out = _ck.convrot_w4a4_linear(x, self._q, self._qs, bias=bias, convrot_groupsize=self._qgs,
+                                              lora=fused, qweight_bf6=self._q6)
                 return self._apply_dyn_lora(x, out, self._dyn_rest if fused is not None else None)
 
 else:  # comfy.ops or the backend unavailable

@@ -123,6 +123,15 @@ int cr_int4_convrot_gemm_lora(const void* Xp, const void* Wp, const void* xscale
  * ceil(rows / 256) * 256 * 3K/4 bytes). */
 int cr_int4_to_bf6(const void* src, void* dst, int rows, int K, void* stream);
 
+/* ck_convrot_quant_int4 writing the codes in the B6T layout (a6out holds
+ * ceil(M / 256) * 256 * 3K/4 bytes, padding rows zero) instead of packed
+ * nibbles; same codes and scales.  K % 128 == 0 and K <= cr_max_quant_bf6_k(). */
+int cr_convrot_quant_bf6(const void* x, int in_dtype, void* a6out, void* scaleout, int M, int K, int G,
+                         void* stream);
+
+/* Largest K accepted by cr_convrot_quant_bf6. */
+int cr_max_quant_bf6_k(void);
+
 /* cr_int4_convrot_gemm_ex on B6T operands (A6 from M rows, W6 from N rows); epilogue 0..3. */
 int cr_int4_convrot_gemm_bf6(const void* A6, const void* W6, const void* xscale, const void* wscale,
                              const void* bias, void* out, int M, int N, int K, int epilogue, void* stream);

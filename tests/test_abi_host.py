@@ -41,6 +41,7 @@ def test_library_queries_without_gpu(native):
     lib = native.load_library()
     assert lib.cr_abi_version() == 2
     assert lib.cr_max_quant_k() == 32768
+    assert lib.cr_max_quant_bf6_k() == 12288
 
 
 def test_argument_errors_return_minus_one(native):
@@ -63,6 +64,11 @@ def test_argument_errors_return_minus_one(native):
     assert lib.cr_int4_convrot_gemm_lora(n, n, n, n, n, n, n, 32, f, n, 4, 4, 64, 3, n) == -1  # acc dump
     assert lib.cr_int4_convrot_gemm_lora(n, n, n, n, n, n, n, 32, f, n, 4, 4, 64, 0, n) == -1  # null t/U
     assert lib.cr_int4_convrot_gemm_lora(n, n, n, n, n, n, n, 64, f, n, 4, 4, 48, 0, n) == -1  # K % 32
+    assert lib.cr_convrot_quant_bf6(n, 1, n, n, 4, 192, 64, n) == -1          # K % 128
+    assert lib.cr_convrot_quant_bf6(n, 1, n, n, 4, 16384, 256, n) == -1       # above the bf6 quantizer's K
+    assert lib.cr_int4_to_bf6(n, n, 4, 96, n) == -1                           # K % 128
+    assert lib.cr_int4_convrot_gemm_bf6(n, n, n, n, n, n, 4, 4, 192, 0, n) == -1
+    assert lib.cr_int4_convrot_gemm_bf6(n, n, n, n, n, n, 4, 4, 256, 4, n) == -1
 
 
 def test_pick_groupsize(backend):

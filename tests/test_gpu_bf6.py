@@ -115,3 +115,63 @@ def test_bf6_lora_equals_int8_path(native, gpu, M, N, K, R):
         o6 = native.int4_convrot_gemm_bf6_lora(a6, w6, cu(xs), cu(ws), cu(b), t, U, 0.7, epi)
         v = (lambda o: o.view(torch.int16) if o.dtype == torch.bfloat16 else o.view(torch.int32))
         assert torch.equal(v(o6), v(o8)), epi
+
+
+QUANT_CASES = [(1, 128, 16, torch.bfloat16), (37, 256, 256, torch.bfloat16), (300, 3072, 256, torch.bfloat16),
+               (4608, 3072, 256, torch.bfloat16), (257, 12288, 256, torch.bfloat16), (64, 1024, 64, torch.bfloat16),
+               (19, 3072, 256, torch.float16), (33, 640, 64, torch.float32), (513, 5120, 256, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("M,K,G,dt", QUANT_CASES)
+def test_quant_bf6_equals_int4_quantizer(native, gpu, M, K, G, dt):
+    """The fused quantizer into B6T writes the same codes and scales as the
+    packed-int4 quantizer (whose parity with the oracle is tested separately),
+    and zero codes in the padding rows."""
+    print(f"quant_bf6 M={M} K={K} G={G} {dt}", flush=True)
+    from inputs import outlier_activations
+    x = outlier_activations(M, K, seed=M + K + G, student_t=True, dtype=dt).cuda()
+    a6, s6 = native.convrot_quant_bf6(x, G)
+    q, s = native.convrot_quant_int4(x, G)
+    assert torch.equal(s6.view(torch.int32), s.view(torch.int32))
+    assert np.array_equal(decode_b6t(a6.cpu().numpy(), M), unpack_int4(q.cpu().numpy()))
+
+
+def test_quant_bf6_zero_rows_and_repeat(native, gpu):
+    """All-zero rows (clamped scale) and a second call on a recycled buffer."""
+    x = torch.zeros(300, 256, dtype=torch.bfloat16, device="cuda")
+    x[5] = 1.0
+    a, s = native.convrot_quant_bf6(x, 256)
+    q, s4 = native.convrot_quant_int4(x, 256)
+    assert torch.equal(s, s4)
+    assert np.array_equal(decode_b6t(a.cpu().numpy(), 300), unpack_int4(q.cpu().numpy()))
+
+
+@pytest.mark.parametrize("M,N,K,G,lora", [(77, 256, 3072, 256, False), (4608, 3072, 3072, 256, False),
+                                          (300, 520, 1024, 64, True), (64, 3072, 12288, 256, False),
+                                          (129, 384, 3072, 256, True)])
+def test_linear_bf6_bit_identical_to_int8_path(backend, native, gpu, M, N, K, G, lora):
+    """convrot_w4a4_linear on the bf6 GEMM (prepared weight) returns exactly
+    the int8-MFMA path's output, LoRA term included."""
+    print(f"linear bf6 M={M} N={N} K={K} lora={lora}", flush=True)
+    from inputs import normal_bias, normal_weight, outlier_activations
+    x = outlier_activations(M, K, seed=M).cuda()
+    qw, ws = backend.quantize_convrot_w4a4_weight(normal_weight(N, K, seed=N).cuda(), convrot_groupsize=G)
+    bias = normal_bias(N, seed=5).cuda()
+    w6 = backend.prepare_convrot_w4a4_weight_bf6(qw)
+    assert w6 is not None and w6.shape == (native.bf6_rows(N), K * 3 // 4)
+    fused = None
+    if lora:
+        rng = np.random.RandomState(K)
+        d = torch.from_numpy((rng.standard_normal((32, K)) * 0.02).astype(np.float32)).cuda()
+        u = torch.from_numpy((rng.standard_normal((N, 32)) * 0.1).astype(np.float32)).cuda()
+        fused = backend.fuse_lora_pairs([(d, u, 0.5)])
+    y6 = backend.convrot_w4a4_linear(x, qw, ws, bias=bias, convrot_groupsize=G, lora=fused, qweight_bf6=w6)
+    y6b = backend.convrot_w4a4_linear(x, qw, ws, bias=bias, convrot_groupsize=G, lora=fused)   # on-the-fly weight
+    qa, xs = native.convrot_quant_int4(x, G)
+    if lora:
+        t = native.lora_down(x, fused[0])
+        y8 = native.int4_convrot_gemm_lora(qa, qw, xs, ws, bias, t, fused[1], 1.0, native.EPI_BF16)
+    else:
+        y8 = native.int4_convrot_gemm(qa, qw, xs, ws, bias, torch.bfloat16)
+    assert torch.equal(y6.view(torch.int16), y8.view(torch.int16))
+    assert torch.equal(y6b.view(torch.int16), y8.view(torch.int16))
