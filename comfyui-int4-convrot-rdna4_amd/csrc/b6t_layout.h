@@ -4,16 +4,22 @@
 // A matrix [rows, K] with K % 128 == 0 is stored with rows padded to a
 // multiple of 256 (zero codes) as [rows/256][K/128] chunks of 24576 bytes;
 // the chunk of (row tile, 128-k block) is one operand half of a GEMM LDS
-// stage, so the GEMM copies it with contiguous 1 KB DMA instructions:
-//   bytes     0..16383  P part: row r at r*64, 16-byte piece p holds dwords
-//                       0..3 of group p ^ f(r) (f: swz below)
-//   bytes 16384..24575  Q part: row r at 16384 + r*32, 8-byte slot s holds
-//                       dwords 4..5 of group s ^ ((r >> 3) & 3)
-// Group g is the MFMA operand of k = 128 kb + 32 g .. +31: 32 BF6 (E3M2,
-// exponent bias 3) codes, code e in bits 6e .. 6e+5 of the 6-dword
-// little-endian bit stream (lane l of v_mfma_*_f8f6f4 supplies row l % 32,
-// k half l / 32).  Both permutations make the GEMM's fragment reads
-// bank-conflict-free.
+// stage, so the GEMM copies it with contiguous 1 KB DMA instructions.
+//
+// Group g of row r is the MFMA operand of k = 128 kb + 32 g .. +31: 32 BF6
+// (E3M2, exponent bias 3) codes, code e in bits 6e .. 6e+5 of 6 little-endian
+// dwords d0..d5 (lane l of v_mfma_*_f8f6f4 supplies row l % 32, k half l / 32).
+// Rows come in 32-row tiles T = r / 32 (r within the chunk) and pairs of
+// tiles 2p, 2p+1; rr = r % 32, f = the swz() row function (depends on rr only):
+//   P part, bytes     0..16383: row r at r*64; 16-byte piece g ^ f holds
+//            d0..d3 of group g when T is even, d2..d5 when T is odd
+//   Q part, bytes 16384..24575: (p, rr) at 16384 + (p*32 + rr)*64; 16-byte
+//            piece g ^ f holds d4..d5 of group g of row 64p + rr (bytes 0..7)
+//            and d0..d1 of group g of row 64p + 32 + rr (bytes 8..15)
+// So a fragment read is conflict-free (the swizzle spreads each 16-lane phase
+// over all 64 banks), one 16-byte Q read serves the fragments of two row
+// tiles, and the registers [P even | Q piece | P odd] hold both 6-dword
+// operands contiguously.
 #pragma once
 
 #include "common.h"
@@ -36,9 +42,13 @@ __host__ __device__ __forceinline__ int swz(int row, int chunk) {
     return chunk ^ ((row >> 1) & 3);
 }
 
-// byte offsets of group g's P and Q pieces for row r (0..255) inside a chunk
+// byte offsets of group g's P piece and of its 16-byte Q piece for row r (0..255)
 __host__ __device__ __forceinline__ int b6_p_off(int r, int g) { return r * 64 + swz(r, g) * 16; }
-__host__ __device__ __forceinline__ int b6_q_off(int r, int g) { return B6_QOFF + r * 32 + 8 * (g ^ ((r >> 3) & 3)); }
+__host__ __device__ __forceinline__ int b6_q_off(int r, int g) {
+    return B6_QOFF + ((r >> 6) * 32 + (r & 31)) * 64 + swz(r, g) * 16;
+}
+// odd 32-row tiles keep dwords d0..d1 in the Q piece (its bytes 8..15)
+__host__ __device__ __forceinline__ bool b6_odd_tile(int r) { return ((r >> 5) & 1) != 0; }
 
 // BF6 code of an integer -8..7: 0 -> 0, |q| = 2^e (1 + m/4) -> (e + 3) << 2 | m, sign 0x20.
 constexpr uint32_t bf6_code_of_int(int q) {

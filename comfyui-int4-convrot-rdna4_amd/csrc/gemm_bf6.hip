@@ -71,12 +71,18 @@ __global__ __launch_bounds__(256) void int4_to_bf6t_kernel(const uint8_t* __rest
         for (int g = 0; g < 4; ++g) in[g] = s[g];
     }
     uint8_t* d = dst + (size_t)tk * B6_CHUNK;
+    const bool odd = b6_odd_tile(r);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         uint32_t c[6];
         encode_group(in[g], c);
-        *reinterpret_cast<uint4*>(d + b6_p_off(r, g)) = make_uint4(c[0], c[1], c[2], c[3]);
-        *reinterpret_cast<uint2*>(d + b6_q_off(r, g)) = make_uint2(c[4], c[5]);
+        if (!odd) {
+            *reinterpret_cast<uint4*>(d + b6_p_off(r, g)) = make_uint4(c[0], c[1], c[2], c[3]);
+            *reinterpret_cast<uint2*>(d + b6_q_off(r, g)) = make_uint2(c[4], c[5]);
+        } else {
+            *reinterpret_cast<uint4*>(d + b6_p_off(r, g)) = make_uint4(c[2], c[3], c[4], c[5]);
+            *reinterpret_cast<uint2*>(d + b6_q_off(r, g) + 8) = make_uint2(c[0], c[1]);
+        }
     }
 }
 
@@ -99,8 +105,13 @@ constexpr int B6_LDS_BYTES = B6_RING_BYTES + EPI_SCALE_FLOATS * 4;
 constexpr int BF6_FMT = 3;                                 // f8f6f4 operand format code of BF6 (E3M2)
 constexpr int E8M0_ONE = 127;                              // block scale 2^0
 
-__device__ __forceinline__ v8i bf6_operand(uint4 p, uint2 q) {
+// operand of an even row tile: d0..d3 from its P piece, d4..d5 from bytes 0..7 of the Q piece
+__device__ __forceinline__ v8i bf6_operand_even(uint4 p, uint4 q) {
     return (v8i){(int)p.x, (int)p.y, (int)p.z, (int)p.w, (int)q.x, (int)q.y, 0, 0};
+}
+// operand of an odd row tile: d0..d1 from bytes 8..15 of the Q piece, d2..d5 from its P piece
+__device__ __forceinline__ v8i bf6_operand_odd(uint4 q, uint4 p) {
+    return (v8i){(int)q.z, (int)q.w, (int)p.x, (int)p.y, (int)p.z, (int)p.w, 0, 0};
 }
 
 template <int EPI, bool LORA>
@@ -129,13 +140,6 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
                                           : W6 + (size_t)(n0 / B6_BN) * nkb * B6_CHUNK;
     const uint8_t* my_src = my_chunks + (wave_u & 3) * (B6_LOADS * 1024) + lane * 16;
     const uint32_t my_lds = (uint32_t)(uintptr_t)lds6 + wave_u * (B6_LOADS * 1024);
-    auto issue = [&](int kb) {
-        const uint32_t st = my_lds + (kb % B6_STAGES) * B6_STAGE_BYTES;
-        const uint8_t* src = my_src + (size_t)kb * B6_CHUNK;
-#pragma unroll
-        for (int j = 0; j < B6_LOADS; ++j) dma16(st + j * 1024, src + j * 1024);
-    };
-
     v16f acc[4][2];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -148,6 +152,10 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
     // k steps (group g = 2 s2 + half).  The P-chunk swizzle and the Q-slot
     // permutation depend only on row bits 1..4, so the fragments of row tiles
     // i = 1..3 sit at fixed distances (i * 2048 in P, i * 1024 in Q).
+    // Per-lane byte offsets of this lane's P pieces and Q pieces inside a stage,
+    // for the two k steps (group g = 2 s2 + half).  The swizzle depends on row
+    // bits 1..4 only, so row tile i sits at i * 2048 in P and tile pair p at
+    // p * 2048 in Q.  The wave's first A and B row tiles are even.
     uint32_t offPa[2], offQa[2], offPb[2], offQb[2];
     {
         const int ra = wm * 128 + frow, rb = wn * 64 + frow;
@@ -160,54 +168,71 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
             offQb[s2] = B6_CHUNK + b6_q_off(rb, g);
         }
     }
-    // one 128-k block from the stage the offsets currently point into: all 12
-    // fragment reads first (both k steps), then the 16 MFMAs, so the second
-    // step's reads complete under the first step's MFMAs
-    auto compute = [&]() {
-        v8i fa[2][4], fb[2][2];
+    // the 6 fragments of k step s2 of the block in the stage at byte offset st:
+    // 6 P reads and 3 Q reads, all 16 bytes
+    auto read_step = [&](uint32_t st, int s2, v8i (&fa)[4], v8i (&fb)[2]) {
+        const uint8_t* base = lds6 + st;
+        uint4 pa[4], pb[2], qa[2], qb;
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
+        for (int i = 0; i < 4; ++i) pa[i] = *reinterpret_cast<const uint4*>(base + offPa[s2] + i * 2048);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                fa[s2][i] = bf6_operand(*reinterpret_cast<const uint4*>(lds6 + offPa[s2] + i * 2048),
-                                        *reinterpret_cast<const uint2*>(lds6 + offQa[s2] + i * 1024));
+        for (int p = 0; p < 2; ++p) qa[p] = *reinterpret_cast<const uint4*>(base + offQa[s2] + p * 2048);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) pb[j] = *reinterpret_cast<const uint4*>(base + offPb[s2] + j * 2048);
+        qb = *reinterpret_cast<const uint4*>(base + offQb[s2]);
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            fa[2 * p] = bf6_operand_even(pa[2 * p], qa[p]);
+            fa[2 * p + 1] = bf6_operand_odd(qa[p], pa[2 * p + 1]);
+        }
+        fb[0] = bf6_operand_even(pb[0], qb);
+        fb[1] = bf6_operand_odd(qb, pb[1]);
+    };
+    auto mfma_step = [&](const v8i (&fa)[4], const v8i (&fb)[2]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
-                fb[s2][j] = bf6_operand(*reinterpret_cast<const uint4*>(lds6 + offPb[s2] + j * 2048),
-                                        *reinterpret_cast<const uint2*>(lds6 + offQb[s2] + j * 1024));
-        }
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(   // transposed tile
+                        fb[j], fa[i], acc[i][j], BF6_FMT, BF6_FMT, 0, E8M0_ONE, 0, E8M0_ONE);
+    };
+    auto issue_clamped = [&](int kb) {     // past the end: re-copy the last block into a free stage
+        const uint32_t st = my_lds + (kb % B6_STAGES) * B6_STAGE_BYTES;
+        const uint8_t* src = my_src + (size_t)min(kb, nkb - 1) * B6_CHUNK;
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(   // transposed tile
-                            fb[s2][j], fa[s2][i], acc[i][j], BF6_FMT, BF6_FMT, 0, E8M0_ONE, 0, E8M0_ONE);
-#ifndef CONVROT_BF6_NO_SCHED
-        // keep that order: the scheduler would otherwise read each fragment just before its MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 18, 0);   // DS reads
-        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);   // MFMAs
-#endif
+        for (int j = 0; j < B6_LOADS; ++j) dma16(st + j * 1024, src + j * 1024);
     };
 
-#pragma unroll
-    for (int p = 0; p < B6_STAGES - 1; ++p)
-        if (p < nkb) issue(p);
+    // Software pipeline across the block barrier.  Per block kb: read the
+    // fragments of k step 1, run the MFMAs of k step 0 (their fragments were read
+    // one phase earlier), wait for block kb+1 and pass the barrier (every wave has
+    // then finished reading block kb, whose stage takes block kb+3), read the
+    // first fragments of block kb+1, run the MFMAs of k step 1.  Each phase's LDS
+    // latency is covered by the other phase's MFMAs, and the loop body is one
+    // branch-free block (sched_barrier(0) pins the phase order; past the end the
+    // copies and reads are harmless repeats).
+    v8i fa0[4], fb0[2], fa1[4], fb1[2];
+    issue_clamped(0);
+    issue_clamped(1);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(B6_LOADS));          // block 0 landed, block 1 in flight
+    __syncthreads();
+    issue_clamped(2);
+    read_step(0, 0, fa0, fb0);
+    uint32_t st_cur = 0;                                      // stage of block kb
     for (int kb = 0; kb < nkb; ++kb) {
-        // block kb landed (blocks kb+1 .. min(kb+B6_STAGES-2, nkb-1) may stay in flight)
-        wait_block_landed<B6_STAGES - 2, B6_LOADS>(min(B6_STAGES - 2, nkb - 1 - kb));
+        const uint32_t st_nxt = st_cur == (B6_STAGES - 1) * B6_STAGE_BYTES ? 0u : st_cur + B6_STAGE_BYTES;
+        read_step(st_cur, 1, fa1, fb1);
+        mfma_step(fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(B6_LOADS));      // block kb+1 landed, block kb+2 in flight
         __syncthreads();
-        if (kb + B6_STAGES - 1 < nkb) issue(kb + B6_STAGES - 1);
-        compute();
-        // advance the fragment offsets to the next stage of the ring (wave-uniform delta)
-        const uint32_t delta = (kb % B6_STAGES == B6_STAGES - 1) ? (uint32_t)(-(B6_STAGES - 1) * B6_STAGE_BYTES)
-                                                                 : (uint32_t)B6_STAGE_BYTES;
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-            offPa[s2] += delta; offQa[s2] += delta; offPb[s2] += delta; offQb[s2] += delta;
-        }
+        issue_clamped(kb + 3);
+        read_step(st_nxt, 0, fa0, fb0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_step(fa1, fb1);
+        st_cur = st_nxt;
     }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));                 // the copies past the end have landed
 
     __syncthreads();                                     // every wave is done with the stages
     // keep the epilogue's index arithmetic out of the main loop's registers

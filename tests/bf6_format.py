@@ -1,12 +1,13 @@
 """numpy decoder of the B6T operand layout of the bf6 GEMM path (test helper).
 
 B6T of a [rows, K] matrix (K % 128 == 0): rows padded to R = ceil(rows/256)*256
-(zero codes), stored as [R/256][K/128] chunks of 24576 bytes.  In a chunk, row
-r holds 64 bytes at r*64 (16-byte piece p: dwords 0..3 of group p ^ f(r),
-f(r) = ((r>>1 ^ r>>3) & 1) | (r>>1 & 2)) and 32 bytes at 16384 + r*32 (8-byte
-slot s: dwords 4..5 of group s ^ ((r>>3) & 3)); group g = the 32 BF6 (E3M2,
-bias 3) codes of k = 128 kb + 32 g .. +31, code e at bits 6e .. 6e+5 of the
-group's 6 little-endian dwords."""
+(zero codes), stored as [R/256][K/128] chunks of 24576 bytes.  Group g of row r
+= the 32 BF6 (E3M2, bias 3) codes of k = 128 kb + 32 g .. +31, code e at bits
+6e .. 6e+5 of 6 little-endian dwords d0..d5.  In a chunk, with T = r // 32,
+rr = r % 32 and f(rr) = ((rr>>1 ^ rr>>3) & 1) | (rr>>1 & 2): the 16-byte piece
+g ^ f(rr) at r*64 holds d0..d3 (T even) or d2..d5 (T odd); the 16-byte piece
+g ^ f(rr) at 16384 + ((r // 64)*32 + rr)*64 holds d4..d5 of the even-tile row
+64p + rr (bytes 0..7) and d0..d1 of the odd-tile row 64p + 32 + rr (bytes 8..15)."""
 import numpy as np
 
 CHUNK = 24576
@@ -36,14 +37,18 @@ def decode_b6t(b6: np.ndarray, rows: int) -> np.ndarray:
     nkb = K // 128
     ch = flat.reshape(R // 256, nkb, CHUNK)
     r = np.arange(256)
-    P = ch[:, :, :QOFF].reshape(R // 256, nkb, 256, 4, 16)
-    Q = ch[:, :, QOFF:].reshape(R // 256, nkb, 256, 4, 8)
+    rr = r % 32
+    odd = (r // 32) % 2 == 1
     g = np.arange(4)
-    pidx = g[None, :] ^ p_row_fn(r)[:, None]                  # [256, 4] physical piece of group g
-    qidx = g[None, :] ^ ((r >> 3) & 3)[:, None]
-    Pg = P[:, :, r[:, None], pidx]                             # [T, nkb, 256, 4, 16]
-    Qg = Q[:, :, r[:, None], qidx]                             # [T, nkb, 256, 4, 8]
-    grp = np.concatenate([Pg, Qg], axis=-1)                    # [T, nkb, 256, 4, 24]
+    piece = g[None, :] ^ p_row_fn(rr)[:, None]                         # [256, 4]
+    P = ch[:, :, :QOFF].reshape(R // 256, nkb, 256, 4, 16)
+    Q = ch[:, :, QOFF:].reshape(R // 256, nkb, 128, 4, 16)
+    qrow = (r // 64) * 32 + rr                                          # Q row of row r
+    Pg = P[:, :, r[:, None], piece]                                     # [T, nkb, 256, 4, 16]
+    Qg = Q[:, :, qrow[:, None], piece]                                  # [T, nkb, 256, 4, 16]
+    even_bytes = np.concatenate([Pg, Qg[..., :8]], axis=-1)             # d0..d3 | d4..d5
+    odd_bytes = np.concatenate([Qg[..., 8:], Pg], axis=-1)              # d0..d1 | d2..d5
+    grp = np.where(odd[None, None, :, None, None], odd_bytes, even_bytes)   # [T, nkb, 256, 4, 24]
     bits = np.unpackbits(grp, axis=-1, bitorder="little")
     code = (bits.reshape(*grp.shape[:-1], 32, 6) * (1 << np.arange(6))).sum(-1)   # [T, nkb, 256, 4, 32]
     vals = bf6_value(code)

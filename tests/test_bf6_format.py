@@ -26,17 +26,23 @@ def encode_b6t(q: np.ndarray) -> np.ndarray:
     out = np.zeros(R * K * 3 // 4, np.uint8)
     for row in range(rows):
         t, r = divmod(row, 256)
+        rr, odd = r % 32, (r // 32) % 2 == 1
         for kb in range(nkb):
             base = (t * nkb + kb) * CHUNK
             for g in range(4):
                 bits = 0
                 for e in range(32):
                     bits |= enc(int(q[row, kb * 128 + 32 * g + e])) << (6 * e)
-                by = np.frombuffer(bits.to_bytes(24, "little"), np.uint8)
-                p = g ^ f(r)
-                out[base + r * 64 + 16 * p: base + r * 64 + 16 * p + 16] = by[:16]
-                s = g ^ ((r >> 3) & 3)
-                out[base + QOFF + r * 32 + 8 * s: base + QOFF + r * 32 + 8 * s + 8] = by[16:]
+                dw = np.frombuffer(bits.to_bytes(24, "little"), np.uint8)      # d0..d5
+                piece = g ^ f(rr)
+                p_at = base + r * 64 + 16 * piece
+                q_at = base + QOFF + ((r // 64) * 32 + rr) * 64 + 16 * piece
+                if not odd:
+                    out[p_at:p_at + 16] = dw[0:16]
+                    out[q_at:q_at + 8] = dw[16:24]
+                else:
+                    out[p_at:p_at + 16] = dw[8:24]
+                    out[q_at + 8:q_at + 16] = dw[0:8]
     return out
 
 
