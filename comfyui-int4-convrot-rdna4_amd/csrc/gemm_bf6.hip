@@ -239,7 +239,7 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
     int em0 = m0, en0 = n0, elane = lane;
     asm volatile("" : "+s"(M), "+s"(N), "+v"(em0), "+v"(en0), "+v"(elane));
     constexpr int SCR = B6_RING_BYTES / (B6_THREADS / 64);
-    epilogue_lds<EPI, 4, 2, LORA, SCR>(acc, sc, bias != nullptr, out, M, N, em0, en0, em0 + wm * 128,
+    epilogue_lds<EPI, 4, 2, LORA, SCR>(acc, sc, out, M, N, em0, en0, em0 + wm * 128,
                                        en0 + wn * 64, elane, lora, lds6 + wave * SCR);
 }
 

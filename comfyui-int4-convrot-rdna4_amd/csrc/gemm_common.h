@@ -37,6 +37,9 @@ __device__ __forceinline__ float acc_float(float v) { return v; }   // an exact 
 
 // Per-tile epilogue scales staged in LDS by the workgroup at kernel start:
 // xs of the tile's 256 rows, ws and bias of its 256 columns (0 outside M / N).
+// A missing bias is staged as -0.0, which makes the epilogue's bias add an
+// exact identity (x + -0 == x for every float, -0 included), so the epilogue
+// needs no per-element select.
 constexpr int EPI_SCALE_FLOATS = 3 * 256;
 __device__ __forceinline__ void stage_scales(float* sc, const float* __restrict__ xs, const float* __restrict__ ws,
                                              const float* __restrict__ bias, int M, int N, int m0, int n0,
@@ -46,7 +49,7 @@ __device__ __forceinline__ void stage_scales(float* sc, const float* __restrict_
         float v = 0.0f;
         if (part == 0) { if (xs && m0 + k < M) v = xs[m0 + k]; }
         else if (part == 1) { if (ws && n0 + k < N) v = ws[n0 + k]; }
-        else { if (bias && n0 + k < N) v = bias[n0 + k]; }
+        else { v = (bias && n0 + k < N) ? bias[n0 + k] : -0.0f; }   // x + (-0) == x for every x, -0 included
         sc[i] = v;
     }
 }
@@ -128,7 +131,7 @@ __device__ __forceinline__ void epilogue_tiles(const AccV (&acc)[FMT][FNT], cons
 // of PT row tiles that fit SCR_BYTES.  `scr` must be 16-byte aligned and owned
 // by this wave; `sc` holds the workgroup tile's staged scales (stage_scales).
 template <int EPI, int FMT, int FNT, bool LORA, int SCR_BYTES, typename AccV>
-__device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const float* sc, bool has_bias,
+__device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const float* sc,
                                              void* __restrict__ out, int M, int N, int tile_m0, int tile_n0,
                                              int row0, int col0, int lane, const LoraArgs& la, uint8_t* scr) {
     constexpr int ES = (EPI == EPI_BF16 || EPI == EPI_BF16_EAGER) ? 2 : 4;
@@ -142,6 +145,20 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
     const int h = lane >> 5;
     const int l32 = lane & 31;
     const bool vec = ((size_t)N * ES) % 16 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+    // per-lane column scales and biases of the 4 quads of each column tile
+    float wv[FNT][4][4], bvv[FNT][4][4];
+    if constexpr (EPI != EPI_ACC) {
+#pragma unroll
+        for (int j = 0; j < FNT; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int c = col0 - tile_n0 + j * 32 + 4 * h + 8 * q;
+                const float4 w4 = *reinterpret_cast<const float4*>(sc + 256 + c);
+                const float4 b4 = *reinterpret_cast<const float4*>(sc + 512 + c);
+                wv[j][q][0] = w4.x; wv[j][q][1] = w4.y; wv[j][q][2] = w4.z; wv[j][q][3] = w4.w;
+                bvv[j][q][0] = b4.x; bvv[j][q][1] = b4.y; bvv[j][q][2] = b4.z; bvv[j][q][3] = b4.w;
+            }
+    }
 #pragma unroll
     for (int i0 = 0; i0 < FMT; i0 += PT) {
 #pragma unroll
@@ -163,13 +180,8 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
                         lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, lacc, 0, 0, 0);   // transposed
                     }
                 }
-                const int cbase = col0 - tile_n0 + j * 32 + 4 * h;       // first column of quad 0
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const float4 w4 = *reinterpret_cast<const float4*>(sc + 256 + cbase + 8 * q);
-                    const float4 b4 = *reinterpret_cast<const float4*>(sc + 512 + cbase + 8 * q);
-                    const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
-                    const float bvv[4] = {b4.x, b4.y, b4.z, b4.w};
                     uint8_t* dst = scr + (ii * 32 + l32) * RS + (j * 32 + 8 * q + 4 * h) * ES;
                     if constexpr (EPI == EPI_ACC) {
                         *reinterpret_cast<int4*>(dst) = make_int4(acc_int(acc[i][j][4 * q]), acc_int(acc[i][j][4 * q + 1]),
@@ -181,13 +193,13 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
                             const float a = acc_float(acc[i][j][4 * q + e]);
                             if constexpr (EPI == EPI_BF16_EAGER) {
                                 float t = bf16r(bf16r(a) * bf16r(xsv));
-                                t = bf16r(t * bf16r(wv[e]));
-                                if (has_bias) t = bf16r(t + bf16r(bvv[e]));
+                                t = bf16r(t * bf16r(wv[j][q][e]));
+                                t = bf16r(t + bf16r(bvv[j][q][e]));                 // -0 when there is no bias
                                 if constexpr (LORA) t = bf16r(t + bf16r(__fmul_rn(la.scale, lacc[4 * q + e])));
                                 v[e] = t;
                             } else {
-                                float t = __fmul_rn(__fmul_rn(a, xsv), wv[e]);
-                                if (has_bias) t = __fadd_rn(t, bvv[e]);
+                                float t = __fmul_rn(__fmul_rn(a, xsv), wv[j][q][e]);
+                                t = __fadd_rn(t, bvv[j][q][e]);                     // -0 when there is no bias
                                 if constexpr (LORA) t = __fadd_rn(t, __fmul_rn(la.scale, lacc[4 * q + e]));
                                 v[e] = t;
                             }
