@@ -111,12 +111,15 @@ int cr_int4_convrot_gemm_lora(const void* Xp, const void* Wp, const void* xscale
  *
  * "B6T" layout of a [rows, K] operand (K % 128 == 0): rows padded to
  * R = ceil(rows / 256) * 256 with zero codes; R * 3K/4 bytes stored as
- * [R / 256][K / 128] chunks of 24576 bytes (256 rows x 128 k).  In a chunk,
- * row r holds 64 bytes at r * 64 (16-byte piece p: dwords 0..3 of group
- * p ^ f(r), f(r) = ((r >> 1 ^ r >> 3) & 1) | (r >> 1 & 2)) and 32 bytes at
- * 16384 + r * 32 (8-byte slot s: dwords 4..5 of group s ^ ((r >> 3) & 3)),
- * group g being the 32 BF6 codes of k = 128 kb + 32 g .. +31, code e at bits
- * 6e..6e+5 of the group's 6 little-endian dwords.
+ * [R / 256][K / 128] chunks of 24576 bytes (256 rows x 128 k).  Group g of a
+ * row is the 32 BF6 codes of k = 128 kb + 32 g .. +31, code e at bits
+ * 6e..6e+5 of the group's 6 little-endian dwords d0..d5.  In a chunk, with
+ * rr = r % 32 and f(rr) = ((rr >> 1 ^ rr >> 3) & 1) | (rr >> 1 & 2):
+ *   bytes 0..16383: row r at r * 64; 16-byte piece g ^ f(rr) holds d0..d3 of
+ *     group g when r / 32 is even, d2..d5 when it is odd;
+ *   bytes 16384..24575: pair p = r / 64 at 16384 + (p * 32 + rr) * 64;
+ *     16-byte piece g ^ f(rr) holds d4..d5 of group g of row 64p + rr
+ *     (bytes 0..7) and d0..d1 of group g of row 64p + 32 + rr (bytes 8..15).
  */
 
 /* Packed int4 [rows, K/2] (the _int4/_codec.py layout) -> B6T (dst holds
