@@ -95,12 +95,18 @@ def main():
                     help="GEMM path: bf6 matrix cores (the Linear's) or packed int4 on int8 MFMA")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (counter calibration)")
+    ap.add_argument("--workload", choices=("block-linears", "dit8"), default="block-linears",
+                    help="block-linears: the four linears of one DiT block (the headline line); "
+                         "dit8: the synthetic 8-block double-stream DiT stack through Int4ConvRotOps")
     args = ap.parse_args()
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (every box here has one); --gpus {args.gpus} "
               "is not supported", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "dit8":
+        bench_dit(args)
+        return
 
     import torch
     importlib.import_module("comfyui-int4-convrot-rdna4_amd")
@@ -246,6 +252,169 @@ def main():
     }
     if copy_cal:
         line["copy_calibration"] = copy_cal
+    print(json.dumps(line), flush=True)
+
+
+DIT_IMG, DIT_TXT, DIT_DEPTH, DIT_RANK = 4096, 512, 8, 32
+
+
+def bench_dit(args):
+    """The synthetic 8-block double-stream DiT stack (hidden 3072, 24 heads,
+    MLP ratio 4; 4096 image + 512 text tokens) loaded through Int4ConvRotOps
+    with the Flux 2 skip list and a rank-32 dynamic LoRA on each of its 64
+    quantized linears.  One step = one forward.  Reports the forward time, the
+    GPU time inside the quantized linears (HIP events around each call), the
+    same linears' kernels replayed back to back through the C-ABI (rotate+quant,
+    LoRA down projection, GEMM with the LoRA epilogue) and the difference: the
+    per-layer cost of the Linear replacement's host path (casts, allocation,
+    launch gaps)."""
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import dit_stack as ds
+    from fake_comfy import FakeLoRA, install_fake_comfy
+    install_fake_comfy()
+    importlib.import_module("comfyui-int4-convrot-rdna4_amd")
+    native = importlib.import_module("comfyui-int4-convrot-rdna4_amd._int4.native")
+    if not native.is_available():
+        raise SystemExit("libconvrot_gfx950.so is not loadable on a gfx950 device; nothing to measure")
+    ops_mod = importlib.import_module("comfyui-int4-convrot-rdna4_amd.int4_ops")
+    if ops_mod.Int4ConvRotOps is None:
+        ops_mod = importlib.reload(ops_mod)
+    Ops = ops_mod.Int4ConvRotOps
+
+    t0 = time.perf_counter()
+    model, _, patches, applied = ds.build_int4_stack(Ops, FakeLoRA, depth=DIT_DEPTH, n_lora_rank=DIT_RANK,
+                                                     keep_reference=False)
+    torch.cuda.synchronize()
+    load_s = time.perf_counter() - t0
+    qlayers = [(n, m) for n, m in model.named_modules() if hasattr(m, "in_features") and ds.is_quantized_name(n)]
+    assert all(m._qmode == "int4" and m._dyn_fused is not None for _, m in qlayers) and applied == set(patches)
+    img, ctx, tt = ds.synthetic_inputs(DIT_IMG, DIT_TXT, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            model(img, ctx, tt)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        h0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(args.steps):
+            model(img, ctx, tt)
+        e1.record(stream)
+        host_s = (time.perf_counter() - h0) / args.steps
+        torch.cuda.synchronize()
+        ms_fwd = e0.elapsed_time(e1) / args.steps
+
+        # GPU time inside the quantized linears: events around each call
+        evs, inputs = [], {}
+
+        def pre(mod, a, name):
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record(torch.cuda.current_stream())
+            evs.append([name, ev, None])
+            inputs.setdefault(name, a[0])
+
+        def post(mod, a, out):
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record(torch.cuda.current_stream())
+            evs[-1][2] = ev
+
+        hooks = []
+        for n, m in qlayers:
+            hooks.append(m.register_forward_pre_hook(lambda mod, a, n=n: pre(mod, a, n)))
+            hooks.append(m.register_forward_hook(post))
+        n_instr = 3
+        for _ in range(n_instr):
+            model(img, ctx, tt)
+        torch.cuda.synchronize()
+        for h in hooks:
+            h.remove()
+        lin_ms = sum(a.elapsed_time(b) for _, a, b in evs) / n_instr
+
+        # the same linears' kernels, replayed back to back through the C-ABI
+        lib = native.load_library()
+        sptr = ctypes.c_void_p(stream.cuda_stream)
+        vp = ctypes.c_void_p
+        calls = []
+        keep = []
+        for n, m in qlayers:
+            x = inputs[n].reshape(-1, m.in_features).contiguous()
+            M, K, N = x.shape[0], m.in_features, m.out_features
+            D, U = m._dyn_fused
+            R = D.shape[0]
+            a6 = torch.empty((native.bf6_rows(M), K // 4 * 3), dtype=torch.uint8, device="cuda")
+            xs = torch.empty((M,), dtype=torch.float32, device="cuda")
+            t = torch.empty((M, R), dtype=torch.bfloat16, device="cuda")
+            out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+            b32 = m.bias.float().contiguous()
+            keep += [x, a6, xs, t, out, b32]
+            calls.append(("rq", lib.cr_convrot_quant_bf6, (vp(x.data_ptr()), 1, vp(a6.data_ptr()),
+                                                           vp(xs.data_ptr()), M, K, m._qgs, sptr)))
+            calls.append(("lora_down", lib.cr_lora_down, (vp(x.data_ptr()), 1, vp(D.data_ptr()), vp(t.data_ptr()),
+                                                          M, K, R, sptr)))
+            calls.append(("gemm_lora", lib.cr_int4_convrot_gemm_bf6_lora,
+                          (vp(a6.data_ptr()), vp(m._q6.data_ptr()), vp(xs.data_ptr()), vp(m._qs.data_ptr()),
+                           vp(b32.data_ptr()), vp(t.data_ptr()), vp(U.data_ptr()), R, ctypes.c_float(1.0),
+                           vp(out.data_ptr()), M, N, K, 1, sptr)))
+            calls.append(("gemm_plain", lib.cr_int4_convrot_gemm_bf6,
+                          (vp(a6.data_ptr()), vp(m._q6.data_ptr()), vp(xs.data_ptr()), vp(m._qs.data_ptr()),
+                           vp(b32.data_ptr()), vp(out.data_ptr()), M, N, K, 1, sptr)))
+        kern = {}
+        reps = 3
+        for rep in range(reps + 1):
+            pairs = []
+            for kind, fn, a in calls:
+                ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                ea.record(stream)
+                rc = fn(*a)
+                eb.record(stream)
+                if rc != 0:
+                    raise RuntimeError(f"{kind} launch failed rc={rc}")
+                pairs.append((kind, ea, eb))
+            torch.cuda.synchronize()
+            if rep > 0:
+                for kind, ea, eb in pairs:
+                    kern[kind] = kern.get(kind, 0.0) + ea.elapsed_time(eb) / reps
+        del keep
+
+    work = ds.quantized_work(DIT_IMG, DIT_TXT, depth=DIT_DEPTH)
+    work_lora = ds.quantized_work(DIT_IMG, DIT_TXT, depth=DIT_DEPTH, lora_rank=DIT_RANK)
+    kern_ms = kern["rq"] + kern["lora_down"] + kern["gemm_lora"]
+    line = {
+        "metric": "DiT stack forward: quantized-linear TOPS inside the forward (8 double blocks, LoRA r32)",
+        "value": round(work / (lin_ms * 1e-3) / 1e12, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_fwd, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": "synthetic double-stream DiT stack through Int4ConvRotOps: 8 blocks, hidden 3072, 24 heads, "
+                        "MLP ratio 4, 4096 image + 512 text tokens, Flux 2 skip list kept bf16, rank-32 dynamic "
+                        "LoRA fused on the 64 quantized linears, weights N(0, 0.02)",
+            "image_tokens": DIT_IMG, "text_tokens": DIT_TXT, "depth": DIT_DEPTH, "lora_rank": DIT_RANK,
+            "quantized_linears": len(qlayers),
+        },
+        "forward_ms": round(ms_fwd, 3),
+        "host_ms_per_forward": round(host_s * 1e3, 3),
+        "quantized_linear_ms": round(lin_ms, 3),
+        "other_ms": round(ms_fwd - lin_ms, 3),
+        "kernels_ms": {k: round(v, 3) for k, v in kern.items()},
+        "kernel_only_linear_ms": round(kern_ms, 3),
+        "linear_overhead_ms": round(lin_ms - kern_ms, 3),
+        "linear_overhead_us_per_layer": round((lin_ms - kern_ms) * 1e3 / len(qlayers), 2),
+        "lora_cost_ms": round(kern["lora_down"] + kern["gemm_lora"] - kern["gemm_plain"], 3),
+        "quantized_TOP_per_forward": round(work / 1e12, 3),
+        "quantized_TOP_per_forward_with_lora": round(work_lora / 1e12, 3),
+        "kernel_only_TOPS": round(work / (kern_ms * 1e-3) / 1e12, 1),
+        "load_s": round(load_s, 2),
+    }
     print(json.dumps(line), flush=True)
 
 

@@ -26,7 +26,9 @@ def rand_bf16(shape, seed, std):
 
 
 DOWN_CASES = [(1, 256, 32, torch.bfloat16), (31, 3072, 64, torch.bfloat16), (33, 2080, 96, torch.float16),
-              (300, 3072, 128, torch.bfloat16), (4608, 3072, 128, torch.bfloat16), (100, 12288, 32, torch.float16)]
+              (300, 3072, 128, torch.bfloat16), (4608, 3072, 128, torch.bfloat16), (100, 12288, 32, torch.float16),
+              (7, 1040, 32, torch.bfloat16), (17, 528, 64, torch.bfloat16), (4096, 12288, 32, torch.bfloat16),
+              (512, 3072, 32, torch.float16), (16, 16, 96, torch.bfloat16)]
 
 
 @pytest.mark.parametrize("M,K,R,dt", DOWN_CASES)
@@ -44,6 +46,7 @@ def test_lora_down_matches_fp64(native, gpu, M, K, R, dt):
     bound = 2.0 ** -8 * np.abs(ref) + (2.0 ** -12 + (2.0 ** -9 if dt == torch.float16 else 0.0)) * mag
     assert np.all(err <= bound), float((err / np.maximum(bound, 1e-30)).max())
     assert np.linalg.norm(f64(t) - ref) / np.linalg.norm(ref) < 4e-3
+    assert torch.equal(native.lora_down(x.cuda(), D.cuda()), t)     # fixed summation order
 
 
 def rand_gemm(M, N, K, R, seed):
