@@ -269,7 +269,7 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
 
     __syncthreads();                                     // every wave is done with the stages
     constexpr int SCR = P_STAGES * P_STAGE_BYTES / (2 * WN);
-    epilogue_lds<EPI, 4, PFN, LORA, SCR>(acc, sc, out, M, N, m0, n0, m0 + wm * 128,
+    epilogue_lds<EPI, 4, PFN, (LORA ? -1 : 0), SCR>(acc, sc, out, M, N, m0, n0, m0 + wm * 128,
                                          n0 + wn * WTN_P, lane, lora, plds + wave * SCR);
 }
 

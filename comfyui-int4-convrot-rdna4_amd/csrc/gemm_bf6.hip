@@ -114,7 +114,7 @@ __device__ __forceinline__ v8i bf6_operand_odd(uint4 q, uint4 p) {
     return (v8i){(int)q.z, (int)q.w, (int)p.x, (int)p.y, (int)p.z, (int)p.w, 0, 0};
 }
 
-template <int EPI, bool LORA>
+template <int EPI, int LR>
 __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
         const uint8_t* __restrict__ A6, const uint8_t* __restrict__ W6,
         const float* __restrict__ xs, const float* __restrict__ ws, const float* __restrict__ bias,
@@ -239,11 +239,11 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
     int em0 = m0, en0 = n0, elane = lane;
     asm volatile("" : "+s"(M), "+s"(N), "+v"(em0), "+v"(en0), "+v"(elane));
     constexpr int SCR = B6_RING_BYTES / (B6_THREADS / 64);
-    epilogue_lds<EPI, 4, 2, LORA, SCR>(acc, sc, out, M, N, em0, en0, em0 + wm * 128,
+    epilogue_lds<EPI, 4, 2, LR, SCR>(acc, sc, out, M, N, em0, en0, em0 + wm * 128,
                                        en0 + wn * 64, elane, lora, lds6 + wave * SCR);
 }
 
-template <int EPI, bool LORA>
+template <int EPI, int LR>
 static hipError_t launch_bf6(const uint8_t* A6, const uint8_t* W6, const float* xs, const float* ws,
                              const float* bias, void* out, int M, int N, int K, const LoraArgs& la,
                              hipStream_t st) {
@@ -254,13 +254,13 @@ static hipError_t launch_bf6(const uint8_t* A6, const uint8_t* W6, const float* 
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= kMaxDev) return hipErrorInvalidDevice;
     if (!attr_set[dev]) {
-        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_bf6_kernel<EPI, LORA>),
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_bf6_kernel<EPI, LR>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, B6_LDS_BYTES);
         if (e != hipSuccess) return e;
         attr_set[dev] = true;
     }
     const int ntiles = ((M + B6_BM - 1) / B6_BM) * ((N + B6_BN - 1) / B6_BN);
-    hipLaunchKernelGGL((w4a4_gemm_bf6_kernel<EPI, LORA>), dim3(ntiles), dim3(B6_THREADS), B6_LDS_BYTES, st,
+    hipLaunchKernelGGL((w4a4_gemm_bf6_kernel<EPI, LR>), dim3(ntiles), dim3(B6_THREADS), B6_LDS_BYTES, st,
                        A6, W6, xs, ws, bias, out, M, N, K, la, tile_group_rows((M + B6_BM - 1) / B6_BM));
     return hipGetLastError();
 }
@@ -282,20 +282,28 @@ hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, cons
     if (t == nullptr) {
         const LoraArgs none{nullptr, nullptr, 0, 0.0f};
         switch (epi) {
-            case EPI_F32: return launch_bf6<EPI_F32, false>(a, w, xs, ws, bias, out, M, N, K, none, st);
-            case EPI_BF16: return launch_bf6<EPI_BF16, false>(a, w, xs, ws, bias, out, M, N, K, none, st);
-            case EPI_BF16_EAGER: return launch_bf6<EPI_BF16_EAGER, false>(a, w, xs, ws, bias, out, M, N, K, none, st);
-            case EPI_ACC: return launch_bf6<EPI_ACC, false>(a, w, xs, ws, bias, out, M, N, K, none, st);
+            case EPI_F32: return launch_bf6<EPI_F32, 0>(a, w, xs, ws, bias, out, M, N, K, none, st);
+            case EPI_BF16: return launch_bf6<EPI_BF16, 0>(a, w, xs, ws, bias, out, M, N, K, none, st);
+            case EPI_BF16_EAGER: return launch_bf6<EPI_BF16_EAGER, 0>(a, w, xs, ws, bias, out, M, N, K, none, st);
+            case EPI_ACC: return launch_bf6<EPI_ACC, 0>(a, w, xs, ws, bias, out, M, N, K, none, st);
             default: return hipErrorInvalidValue;
         }
     }
     const LoraArgs la{reinterpret_cast<const __bf16*>(t), reinterpret_cast<const __bf16*>(U), R, scale};
-    switch (epi) {
-        case EPI_F32: return launch_bf6<EPI_F32, true>(a, w, xs, ws, bias, out, M, N, K, la, st);
-        case EPI_BF16: return launch_bf6<EPI_BF16, true>(a, w, xs, ws, bias, out, M, N, K, la, st);
-        case EPI_BF16_EAGER: return launch_bf6<EPI_BF16_EAGER, true>(a, w, xs, ws, bias, out, M, N, K, la, st);
+    if (R % 32 != 0 || R < 32 || R > 128) return hipErrorInvalidValue;
+#define BF6_LORA_CASE(LRV)                                                                                      \
+    case LRV:                                                                                                   \
+        switch (epi) {                                                                                          \
+            case EPI_F32: return launch_bf6<EPI_F32, LRV>(a, w, xs, ws, bias, out, M, N, K, la, st);            \
+            case EPI_BF16: return launch_bf6<EPI_BF16, LRV>(a, w, xs, ws, bias, out, M, N, K, la, st);          \
+            case EPI_BF16_EAGER: return launch_bf6<EPI_BF16_EAGER, LRV>(a, w, xs, ws, bias, out, M, N, K, la, st); \
+            default: return hipErrorInvalidValue;                                                               \
+        }
+    switch (R / 32) {
+        BF6_LORA_CASE(1) BF6_LORA_CASE(2) BF6_LORA_CASE(3) BF6_LORA_CASE(4)
         default: return hipErrorInvalidValue;
     }
+#undef BF6_LORA_CASE
 }
 
 }  // namespace convrot

@@ -130,10 +130,21 @@ __device__ __forceinline__ void epilogue_tiles(const AccV (&acc)[FMT][FNT], cons
 // store instruction writes whole row segments.  Rows are processed in passes
 // of PT row tiles that fit SCR_BYTES.  `scr` must be 16-byte aligned and owned
 // by this wave; `sc` holds the workgroup tile's staged scales (stage_scales).
-template <int EPI, int FMT, int FNT, bool LORA, int SCR_BYTES, typename AccV>
+//
+// LR selects the LoRA term: 0 none; -1 rank la.R read at run time (one
+// dependent t / U load pair per 16 ranks and tile); 1..4 rank 32 * LR known at
+// compile time, loaded in batches of 32 ranks (two t and two U fragments) per
+// tile.  For rank 32 with a bf16 output the U fragments of the wave's columns
+// are loaded once and the t fragments of row tile i + 1 while tile i is
+// finished, so the wave waits for L2 about once in all (more registers than
+// the other cases can spare).  The MFMA sequence (16-rank steps in ascending
+// order) is the same in every mode, so are the results.
+template <int EPI, int FMT, int FNT, int LR, int SCR_BYTES, typename AccV>
 __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const float* sc,
                                              void* __restrict__ out, int M, int N, int tile_m0, int tile_n0,
                                              int row0, int col0, int lane, const LoraArgs& la, uint8_t* scr) {
+    constexpr bool LORA = LR != 0;
+    constexpr bool PRE = LR == 1 && (EPI == EPI_BF16 || EPI == EPI_BF16_EAGER);
     constexpr int ES = (EPI == EPI_BF16 || EPI == EPI_BF16_EAGER) ? 2 : 4;
     constexpr int RB = FNT * 32 * ES;                // bytes of one wave-tile row
     constexpr int RS = RB + 16;                      // padded LDS row stride
@@ -145,6 +156,28 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
     const int h = lane >> 5;
     const int l32 = lane & 31;
     const bool vec = ((size_t)N * ES) % 16 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+    // compile-time rank: fragments of 16-rank steps s0, s0 + 1 of row tile i (t) / column tile j (U)
+    constexpr int RK = LR > 0 ? 32 * LR : 32;
+    auto load_t2 = [&](int i, int s0, bf16x8_t (&dst)[2]) {
+        const int trow = row0 + i * 32 + l32;
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+            dst[s] = trow < M ? *reinterpret_cast<const bf16x8_t*>(la.t + (size_t)trow * RK + 16 * (s0 + s) + 8 * h)
+                              : (bf16x8_t){0};
+    };
+    auto load_u2 = [&](int j, int s0, bf16x8_t (&dst)[2]) {
+        const int ucol = col0 + j * 32 + l32;
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+            dst[s] = ucol < N ? *reinterpret_cast<const bf16x8_t*>(la.U + (size_t)ucol * RK + 16 * (s0 + s) + 8 * h)
+                              : (bf16x8_t){0};
+    };
+    bf16x8_t uf[PRE ? FNT : 1][2], tfc[2], tfn[2];
+    if constexpr (PRE) {
+        load_t2(0, 0, tfc);
+#pragma unroll
+        for (int j = 0; j < FNT; ++j) load_u2(j, 0, uf[j]);
+    }
     // per-lane column scales and biases of the 4 quads of each column tile
     float wv[FNT][4][4], bvv[FNT][4][4];
     if constexpr (EPI != EPI_ACC) {
@@ -165,10 +198,27 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
         for (int ii = 0; ii < PT; ++ii) {
             const int i = i0 + ii;
             const float xsv = sc[row0 - tile_m0 + i * 32 + l32];
+            if constexpr (PRE) {
+                if (i + 1 < FMT) load_t2(i + 1, 0, tfn);
+            }
 #pragma unroll
             for (int j = 0; j < FNT; ++j) {
                 f32x16_t lacc = (f32x16_t){0};
-                if constexpr (LORA) {
+                if constexpr (PRE) {
+#pragma unroll
+                    for (int s = 0; s < 2; ++s)
+                        lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(uf[j][s], tfc[s], lacc, 0, 0, 0);   // transposed
+                } else if constexpr (LR > 0) {
+#pragma unroll
+                    for (int c = 0; c < LR; ++c) {                     // 32 ranks per batch of loads
+                        bf16x8_t ta[2], ub[2];
+                        load_t2(i, 2 * c, ta);
+                        load_u2(j, 2 * c, ub);
+#pragma unroll
+                        for (int s = 0; s < 2; ++s)
+                            lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ub[s], ta[s], lacc, 0, 0, 0);   // transposed
+                    }
+                } else if constexpr (LR < 0) {
                     const int trow = row0 + i * 32 + l32;
                     const int ucol = col0 + j * 32 + l32;
                     for (int rk = 0; rk < la.R; rk += 16) {
@@ -211,6 +261,10 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
                         }
                     }
                 }
+            }
+            if constexpr (PRE) {
+                tfc[0] = tfn[0];
+                tfc[1] = tfn[1];
             }
         }
         wave_sync();
