@@ -59,8 +59,14 @@ def gemm_traffic_bytes():
 
 def rq_bytes(M, K, path="bf6"):
     """Algorithmic HBM bytes of one rotate+quant launch: read bf16, write the codes
-    (bf6 layout: 0.75 B per element over rows padded to 256; int4: 0.5 B) + scales."""
-    codes = ((M + 255) // 256 * 256) * K * 3 // 4 if path == "bf6" else M * K // 2
+    (bf6 layout: 0.75 B per element over rows padded to 256; int4: 0.5 B; the W8A8
+    tier's int8: 1 B) + scales."""
+    if path == "bf6":
+        codes = ((M + 255) // 256 * 256) * K * 3 // 4
+    elif path == "w8a8":
+        codes = M * K
+    else:
+        codes = M * K // 2
     return M * K * 2 + codes + 4 * M
 
 
@@ -73,6 +79,8 @@ class Linear:
         w = normal_weight(N, K, seed=seed + 1).to(dev)
         self.qw, self.ws = native.convrot_quant_int4(w, G)         # load-time weight quantization
         self.w6 = native.int4_to_bf6(self.qw)                        # load-time bf6 operand encoding
+        self.qw8, self.ws8 = native.convrot_quant_int8(w, G)       # the int8 tier's weight
+        self.q8 = torch.empty((M_TOKENS, K), dtype=torch.int8, device=dev)
         self.bias = normal_bias(N, seed=seed + 2).to(dev).float()
         self.qx = torch.empty((M_TOKENS, K // 2), dtype=torch.int8, device=dev)
         self.a6 = torch.empty((native.bf6_rows(M_TOKENS), K // 4 * 3), dtype=torch.uint8, device=dev)
@@ -91,8 +99,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time for the oracle baseline (0 disables it)")
-    ap.add_argument("--path", choices=("bf6", "int8"), default="bf6",
-                    help="GEMM path: bf6 matrix cores (the Linear's) or packed int4 on int8 MFMA")
+    ap.add_argument("--path", choices=("bf6", "int8", "w8a8"), default="bf6",
+                    help="GEMM path: bf6 matrix cores (the Linear's), packed int4 on int8 MFMA, or the "
+                         "W8A8 tier (int8 activations and weights on int8 MFMA)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (counter calibration)")
     ap.add_argument("--workload", choices=("block-linears", "dit8"), default="block-linears",
@@ -128,6 +137,12 @@ def main():
                           (vp(L.x.data_ptr()), 1, vp(L.a6.data_ptr()), vp(L.xs.data_ptr()), L.M, L.K, G, sptr)))
             calls.append(("gemm", i, lib.cr_int4_convrot_gemm_bf6,
                           (vp(L.a6.data_ptr()), vp(L.w6.data_ptr()), vp(L.xs.data_ptr()), vp(L.ws.data_ptr()),
+                           vp(L.bias.data_ptr()), vp(L.out.data_ptr()), L.M, L.N, L.K, 1, sptr)))
+        elif args.path == "w8a8":
+            calls.append(("rq", i, lib.ck_convrot_quant_int8,
+                          (vp(L.x.data_ptr()), 1, vp(L.q8.data_ptr()), vp(L.xs.data_ptr()), L.M, L.K, G, sptr)))
+            calls.append(("gemm", i, lib.ck_int8_convrot_gemm,
+                          (vp(L.q8.data_ptr()), vp(L.qw8.data_ptr()), vp(L.xs.data_ptr()), vp(L.ws8.data_ptr()),
                            vp(L.bias.data_ptr()), vp(L.out.data_ptr()), L.M, L.N, L.K, 1, sptr)))
         else:
             calls.append(("rq", i, lib.ck_convrot_quant_int4,
@@ -206,7 +221,7 @@ def main():
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
 
     line = {
-        "metric": METRIC,
+        "metric": METRIC if args.path != "w8a8" else METRIC.replace("W4A4", "W8A8"),
         "value": round(value, 2),
         "unit": "TOPS",
         "n_gpus": 1,
@@ -225,8 +240,9 @@ def main():
             "gemm_path": args.path,
         },
         "roofline": {
-            "kernel": ("w4a4_gemm_bf6_kernel<EPI_BF16> (v_mfma_scale_f32_32x32x64_f8f6f4, BF6 operands)"
-                       if args.path == "bf6" else "w4a4_gemm_pipe_kernel<EPI_BF16> (v_mfma_i32_32x32x32_i8)"),
+            "kernel": {"bf6": "w4a4_gemm_bf6_kernel<EPI_BF16> (v_mfma_scale_f32_32x32x64_f8f6f4, BF6 operands)",
+                       "int8": "w4a4_gemm_pipe_kernel<EPI_BF16> (v_mfma_i32_32x32x32_i8, int4 unpacked)",
+                       "w8a8": "w4a4_gemm_pipe_kernel<EPI_BF16, I8> (v_mfma_i32_32x32x32_i8, int8 operands)"}[args.path],
             "bound": "mfma",
             "achieved": round(gemm_tops, 1),
             "peak": PEAK_FP6_TFLOPS if args.path == "bf6" else PEAK_INT8_TOPS,
@@ -235,8 +251,9 @@ def main():
             "traffic": gemm_traffic_bytes() if args.path == "bf6" else None,
         },
         "rotate_quant": {
-            "kernel": ("rotquant_wave_kernel<bf16,256,3,B6T out>" if args.path == "bf6"
-                       else "rotquant_wave_kernel<bf16,256,3,packed int4 out>"),
+            "kernel": {"bf6": "rotquant_wave_kernel<bf16,256,3,B6T out>",
+                       "int8": "rotquant_wave_kernel<bf16,256,3,packed int4 out>",
+                       "w8a8": "rotquant_wave_kernel<bf16,256,3,int8 out>"}[args.path],
             "bound": "hbm",
             "GBps_at_M4608_K3072": round(metric_rq_gbs, 1),
             "frac_at_M4608_K3072": round(metric_rq_gbs / PEAK_HBM_GBS, 4),

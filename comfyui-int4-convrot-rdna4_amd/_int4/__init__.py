@@ -286,6 +286,30 @@ def fuse_lora_pairs(pairs, device=None):
     return D, U
 
 
-def convrot_w8a8_linear(x, qweight, wscales, bias=None, convrot_groupsize=256):
-    """W8A8 tier (reference _int4/__init__.py:141-175): not built for gfx950 yet."""
-    raise NotImplementedError("the ConvRot W8A8 tier has no gfx950 kernels in this build")
+def convrot_w8a8_linear(
+    x: torch.Tensor,
+    qweight: torch.Tensor,
+    wscales: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    convrot_groupsize: int = 256,
+) -> torch.Tensor:
+    """Compute ``x @ W.T + bias`` with the gfx950 W8A8 ConvRot path (the int8
+    tier, reference _int4/__init__.py:141-175): fused rotate + int8 quantize of
+    x (the eager arithmetic of _int4/int8_eager.py:22-28), then the int8 GEMM
+    with exact int32 accumulation and the fp32 epilogue, both on torch's current
+    stream.  qweight int8 [N, K], wscales [N] f32."""
+    if x.shape[-1] != qweight.shape[-1]:
+        raise ValueError(f"Input K={x.shape[-1]} does not match qweight K={qweight.shape[-1]}")
+    if x.shape[-1] % convrot_groupsize != 0:
+        raise ValueError(f"Input K={x.shape[-1]} not divisible by convrot_groupsize {convrot_groupsize}")
+    _check_groupsize(convrot_groupsize)
+    orig_shape = x.shape
+    x2d = x.reshape(-1, orig_shape[-1]).contiguous()
+    if x2d.dtype not in native._IN_DTYPE_CODE:
+        x2d = x2d.to(torch.float32)
+    qact, x_scale = native.convrot_quant_int8(x2d, convrot_groupsize)
+    out_dtype = x.dtype if x.dtype in _NATIVE_OUT else torch.float32
+    out = native.int8_convrot_gemm(qact, qweight, x_scale, wscales, bias, out_dtype)
+    if out.dtype != x.dtype:
+        out = out.to(x.dtype)
+    return out.reshape(*orig_shape[:-1], qweight.shape[0])

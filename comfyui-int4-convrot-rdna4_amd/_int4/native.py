@@ -41,6 +41,9 @@ _SIGNATURES = {
     "cr_max_quant_bf6_k": ([], _i),
     "cr_int4_convrot_gemm_bf6": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
     "cr_int4_convrot_gemm_bf6_lora": ([_vp] * 7 + [_i, ctypes.c_float, _vp] + [_i] * 4 + [_vp], _i),
+    "ck_convrot_quant_int8": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
+    "ck_int8_convrot_gemm": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
+    "cr_int8_convrot_gemm_ex": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
     "cr_max_quant_k": ([], _i),
     "cr_abi_version": ([], _i),
 }
@@ -373,3 +376,65 @@ def int4_convrot_gemm_bf6_lora(a6, w6, x_scale, w_scale, bias, t, up, scale: flo
     if rc != 0:
         raise RuntimeError(f"cr_int4_convrot_gemm_bf6_lora failed, hipError={rc}")
     return out
+
+
+# ----------------------------------------------------------------------------
+# W8A8 tier (reference _int4/int8_eager.py, hip_loader.py:95-147)
+# ----------------------------------------------------------------------------
+
+def convrot_quant_int8(x: torch.Tensor, convrot_groupsize: int):
+    """Fused ConvRot rotation + rowwise int8 quantize (reference hip_loader.py:95-113).
+
+    Returns (q int8 [M, K], scale f32 [M]).  Supports groupsize 16/64/256."""
+    lib = load_library()
+    if convrot_groupsize not in (16, 64, 256):
+        raise ValueError("fused convrot_quant_int8 supports groupsize 16/64/256")
+    if x.dtype not in _IN_DTYPE_CODE:
+        raise ValueError(f"convrot_quant_int8 input dtype must be f32/bf16/f16, got {x.dtype}")
+    _check_cuda(x)
+    x = _aligned(x)
+    M, K = x.shape
+    qout = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    scale = torch.empty((M,), dtype=torch.float32, device=x.device)
+    rc = lib.ck_convrot_quant_int8(_ptr(x), _IN_DTYPE_CODE[x.dtype], _ptr(qout), _ptr(scale),
+                                   M, K, convrot_groupsize, _stream(x.device))
+    if rc != 0:
+        raise RuntimeError(f"ck_convrot_quant_int8 failed, hipError={rc}")
+    return qout, scale
+
+
+def int8_convrot_gemm_ex(x_int8, w_int8, x_scale, w_scale, bias, epilogue: int):
+    """W8A8 GEMM with epilogue 0 (f32), 1 (bf16) or 3 (int32 accumulators)."""
+    lib = load_library()
+    _check_cuda(x_int8, w_int8, x_scale, w_scale, bias)
+    if x_int8.dtype != torch.int8 or w_int8.dtype != torch.int8:
+        raise ValueError("W8A8 operands must be int8")
+    x_int8, w_int8 = _aligned(x_int8), _aligned(w_int8)
+    M, K = x_int8.shape
+    N, K2 = w_int8.shape
+    if K != K2:
+        raise ValueError(f"K mismatch: x {tuple(x_int8.shape)} w {tuple(w_int8.shape)}")
+    xs = x_scale.to(torch.float32).contiguous() if x_scale is not None else None
+    wsc = w_scale.to(torch.float32).contiguous() if w_scale is not None else None
+    b = bias.to(torch.float32).contiguous() if bias is not None else None
+    odt = {EPI_F32: torch.float32, EPI_BF16: torch.bfloat16, EPI_ACC: torch.int32}[epilogue]
+    out = torch.empty((M, N), dtype=odt, device=x_int8.device)
+    rc = lib.cr_int8_convrot_gemm_ex(_ptr(x_int8), _ptr(w_int8), _ptr(xs), _ptr(wsc), _ptr(b), _ptr(out),
+                                     M, N, K, epilogue, _stream(x_int8.device))
+    if rc != 0:
+        raise RuntimeError(f"cr_int8_convrot_gemm_ex failed, hipError={rc}")
+    return out
+
+
+def int8_gemm_acc(x_int8, w_int8):
+    """Exact int32 accumulators of the W8A8 product."""
+    return int8_convrot_gemm_ex(x_int8, w_int8, None, None, None, EPI_ACC)
+
+
+def int8_convrot_gemm(x_int8, w_int8, x_scale, w_scale, bias, out_dtype):
+    """out[M,N] = (X[M,K] @ W[N,K]^T) * x_scale[:,None] * w_scale[None,:] (+bias)
+    (reference hip_loader.py:116-147); out_dtype float32 or bfloat16."""
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"int8 gemm output dtype must be float32/bfloat16, got {out_dtype}")
+    return int8_convrot_gemm_ex(x_int8, w_int8, x_scale, w_scale, bias,
+                                EPI_F32 if out_dtype == torch.float32 else EPI_BF16)

@@ -19,6 +19,10 @@ hipError_t int4_to_bf6_launch(const void* src, void* dst, int rows, int K, hipSt
 hipError_t rotquant_b6_launch(const void* x, int in_dtype, uint8_t* a6, float* s, int M, int K, int G,
                               hipStream_t st);
 int rotquant_b6_max_k();
+hipError_t rotquant_i8_launch(const void* x, int in_dtype, int8_t* q, float* s, int M, int K, int G,
+                              hipStream_t st);
+hipError_t gemm_i8_launch(const int8_t* X, const int8_t* W, const float* xs, const float* ws,
+                          const float* bias, void* out, int M, int N, int K, int epi, hipStream_t st);
 hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, const float* ws, const float* bias,
                            const void* t, const void* U, int R, float scale, void* out, int M, int N, int K,
                            int epi, hipStream_t st);
@@ -129,6 +133,30 @@ API int cr_int4_convrot_gemm_bf6_lora(const void* A6, const void* W6, const void
                                          epilogue, reinterpret_cast<hipStream_t>(stream));
 }
 
+API int ck_convrot_quant_int8(const void* x, int in_dtype, void* qout, void* scaleout,
+                              int M, int K, int G, void* stream) {
+    if (!quant_args_ok(in_dtype, M, K, G)) return -1;
+    return (int)convrot::rotquant_i8_launch(x, in_dtype, reinterpret_cast<int8_t*>(qout),
+                                            reinterpret_cast<float*>(scaleout), M, K, G,
+                                            reinterpret_cast<hipStream_t>(stream));
+}
+
+API int cr_int8_convrot_gemm_ex(const void* X, const void* W, const void* xscale, const void* wscale,
+                                const void* bias, void* out, int M, int N, int K, int epilogue, void* stream) {
+    if (K % 16 != 0 || K <= 0 || K >= 131072 || M < 0 || N < 0) return -1;
+    if (epilogue != 0 && epilogue != 1 && epilogue != 3) return -1;
+    return (int)convrot::gemm_i8_launch(reinterpret_cast<const int8_t*>(X), reinterpret_cast<const int8_t*>(W),
+                                        reinterpret_cast<const float*>(xscale), reinterpret_cast<const float*>(wscale),
+                                        reinterpret_cast<const float*>(bias), out, M, N, K, epilogue,
+                                        reinterpret_cast<hipStream_t>(stream));
+}
+
+API int ck_int8_convrot_gemm(const void* X, const void* W, const void* xscale, const void* wscale,
+                             const void* bias, void* out, int M, int N, int K, int out_dtype, void* stream) {
+    if (out_dtype != 0 && out_dtype != 1) return -1;
+    return cr_int8_convrot_gemm_ex(X, W, xscale, wscale, bias, out, M, N, K, out_dtype, stream);
+}
+
 API int cr_max_quant_k(void) { return convrot::rotquant_max_k(); }
 
-API int cr_abi_version(void) { return 2; }
+API int cr_abi_version(void) { return 3; }

@@ -16,6 +16,11 @@
 // k order inside one MFMA does not matter as long as A and B use the same
 // permutation, which they do (same loads, same unpack).
 //
+// W8A8 (the reference's int8 tier, _int4/int8_eager.py): with I8 the operands
+// are plain int8 [rows, K] (_int4/int8_eager.py:31-47 storage) and feed the
+// same MFMA unchanged, 64 k per 64-byte LDS row block, accumulating acc itself
+// (|acc| <= 127^2 K < 2^31 for K < 133000).
+//
 // Tiling: a 512-lane workgroup computes a 256 x 256 tile; its 8 waves form a
 // 2 (M) x 4 (N) grid of 128 x 64 wave tiles (4 x 2 MFMA 32x32 tiles).  Packed
 // nibbles are staged through LDS in 128-k blocks (64 bytes per row, rows
@@ -42,7 +47,7 @@ __device__ __forceinline__ void unpack16(uint4 p, v4i& lo_step, v4i& hi_step) {
                     (int)((p.w << 4) & 0xF0F0F0F0u), (int)(p.w & 0xF0F0F0F0u)};
 }
 
-template <int EPI, bool LORA>
+template <int EPI, bool LORA, bool I8>
 __global__ __launch_bounds__(NTHR) void w4a4_gemm_kernel(
         const int8_t* __restrict__ Xp, const int8_t* __restrict__ Wp,
         const float* __restrict__ xs, const float* __restrict__ ws, const float* __restrict__ bias,
@@ -56,8 +61,8 @@ __global__ __launch_bounds__(NTHR) void w4a4_gemm_kernel(
     const int wn = wave & 3;             // 0..3
     const int m0 = blockIdx.y * TBM;
     const int n0 = blockIdx.x * TBN;
-    const int Kb = K / 2;                // packed bytes per row
-    const int nkb = (K + TBK - 1) / TBK;
+    const int Kb = I8 ? K : K / 2;       // operand bytes per row
+    const int nkb = (Kb + ROWB - 1) / ROWB;
 
     // global -> LDS staging: (TBM + TBN) rows x 4 chunks of 16 B = 2048 chunks, 4 per lane
     uint4 stage[4];
@@ -110,7 +115,23 @@ __global__ __launch_bounds__(NTHR) void w4a4_gemm_kernel(
         const uint8_t* la = &lds[buf][0];
         const uint8_t* lb = &lds[buf][TBM * LDS_STRIDE];
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {            // two 64-k slices per block
+        for (int s2 = 0; s2 < 2 && I8; ++s2) {      // W8A8: two 32-k slices per block, bytes used as they are
+            const int koff = s2 * 32 + fhalf * 16;
+            v4i a[FM], b[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                a[i] = *reinterpret_cast<const v4i*>(la + (wm * WTM + i * 32 + frow) * LDS_STRIDE + koff);
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                b[j] = *reinterpret_cast<const v4i*>(lb + (wn * WTN + j * 32 + frow) * LDS_STRIDE + koff);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < 2 && !I8; ++s2) {     // two 64-k slices per block
             const int koff = s2 * 32 + fhalf * 16;
             v4i a_lo[FM], a_hi[FM], b_lo[FN], b_hi[FN];
 #pragma unroll
@@ -135,11 +156,11 @@ __global__ __launch_bounds__(NTHR) void w4a4_gemm_kernel(
         __syncthreads();
     }
 
-    epilogue_tiles<EPI, FM, FN, LORA>(acc, xs, ws, bias, out, M, N, m0 + wm * WTM, n0 + wn * WTN, lane, lora);
+    epilogue_tiles<EPI, FM, FN, LORA, I8 ? 0 : 8>(acc, xs, ws, bias, out, M, N, m0 + wm * WTM, n0 + wn * WTN, lane, lora);
 }
 
 // ---------------------------------------------------------------------------
-// Pipelined kernel (K % 128 == 0).
+// Pipelined kernel (K % 128 == 0; W8A8: K % 64 == 0).
 //
 // 256 x 256 tile per workgroup of 2 x WN waves (default 8 waves of 128 x 64:
 // 4 x 2 MFMA 32x32 tiles each, two waves per SIMD so one wave's unpack and
@@ -167,7 +188,7 @@ constexpr int P_STAGES = CONVROT_PIPE_STAGES;
 constexpr int P_STAGE_BYTES = (P_BM + P_BN) * P_ROWB;  // 32 KB
 constexpr int P_LDS_BYTES = P_STAGES * P_STAGE_BYTES + EPI_SCALE_FLOATS * 4;
 
-template <int EPI, int WN, bool LORA>
+template <int EPI, int WN, bool LORA, bool I8>
 __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
         const int8_t* __restrict__ Xp, const int8_t* __restrict__ Wp,
         const float* __restrict__ xs, const float* __restrict__ ws, const float* __restrict__ bias,
@@ -186,8 +207,8 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
     tile_of_block(blockIdx.x, (M + P_BM - 1) / P_BM, (N + P_BN - 1) / P_BN, gm, tm, tn);
     const int m0 = tm * P_BM;
     const int n0 = tn * P_BN;
-    const int Kb = K / 2;
-    const int nkb = K / P_BK;
+    const int Kb = I8 ? K : K / 2;                      // operand bytes per row
+    const int nkb = Kb / P_ROWB;
     float* sc = reinterpret_cast<float*>(plds + P_STAGES * P_STAGE_BYTES);
     stage_scales(sc, xs, ws, bias, M, N, m0, n0, tid, 128 * WN);   // visible after the loop's first barrier
 
@@ -248,7 +269,17 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
             }
         }
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
+        for (int s2 = 0; s2 < 2 && I8; ++s2) {          // W8A8: the 16 bytes are the operand
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < PFN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i, fb[s2][j]),
+                                                                     __builtin_bit_cast(v4i, fa[s2][i]), acc[i][j],
+                                                                     0, 0, 0);
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < 2 && !I8; ++s2) {
             v4i a_lo[4], a_hi[4], b_lo[PFN], b_hi[PFN];
 #pragma unroll
             for (int i = 0; i < 4; ++i) unpack16(fa[s2][i], a_lo[i], a_hi[i]);
@@ -269,15 +300,15 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
 
     __syncthreads();                                     // every wave is done with the stages
     constexpr int SCR = P_STAGES * P_STAGE_BYTES / (2 * WN);
-    epilogue_lds<EPI, 4, PFN, (LORA ? -1 : 0), SCR>(acc, sc, out, M, N, m0, n0, m0 + wm * 128,
+    epilogue_lds<EPI, 4, PFN, (LORA ? -1 : 0), SCR, I8 ? 0 : 8>(acc, sc, out, M, N, m0, n0, m0 + wm * 128,
                                          n0 + wn * WTN_P, lane, lora, plds + wave * SCR);
 }
 
-template <int EPI, bool LORA>
+template <int EPI, bool LORA, bool I8 = false>
 static hipError_t launch_epi(const int8_t* Xp, const int8_t* Wp, const float* xs, const float* ws,
                              const float* bias, void* out, int M, int N, int K, const LoraArgs& la,
                              hipStream_t st) {
-    if (K % P_BK == 0) {
+    if ((I8 ? K : K / 2) % P_ROWB == 0) {
         constexpr int WN = CONVROT_PIPE_WN;
         const int ntiles = ((M + P_BM - 1) / P_BM) * ((N + P_BN - 1) / P_BN);
         constexpr int kMaxDev = 64;
@@ -287,17 +318,17 @@ static hipError_t launch_epi(const int8_t* Xp, const int8_t* Wp, const float* xs
         if (e != hipSuccess) return e;
         if (dev < 0 || dev >= kMaxDev) return hipErrorInvalidDevice;
         if (!attr_set[dev]) {
-            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_pipe_kernel<EPI, WN, LORA>),
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_pipe_kernel<EPI, WN, LORA, I8>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, P_LDS_BYTES);
             if (e != hipSuccess) return e;
             attr_set[dev] = true;
         }
-        hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<EPI, WN, LORA>), dim3(ntiles), dim3(128 * WN),
+        hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<EPI, WN, LORA, I8>), dim3(ntiles), dim3(128 * WN),
                            P_LDS_BYTES, st, Xp, Wp, xs, ws, bias, out, M, N, K, la,
                            tile_group_rows((M + P_BM - 1) / P_BM));
     } else {
         dim3 grid((N + TBN - 1) / TBN, (M + TBM - 1) / TBM), block(NTHR);
-        hipLaunchKernelGGL((w4a4_gemm_kernel<EPI, LORA>), grid, block, 0, st, Xp, Wp, xs, ws, bias, out, M, N, K, la);
+        hipLaunchKernelGGL((w4a4_gemm_kernel<EPI, LORA, I8>), grid, block, 0, st, Xp, Wp, xs, ws, bias, out, M, N, K, la);
     }
     return hipGetLastError();
 }
@@ -311,6 +342,20 @@ hipError_t gemm_launch(const int8_t* Xp, const int8_t* Wp, const float* xs, cons
         case EPI_BF16: return launch_epi<EPI_BF16, false>(Xp, Wp, xs, ws, bias, out, M, N, K, none, st);
         case EPI_BF16_EAGER: return launch_epi<EPI_BF16_EAGER, false>(Xp, Wp, xs, ws, bias, out, M, N, K, none, st);
         case EPI_ACC: return launch_epi<EPI_ACC, false>(Xp, Wp, xs, ws, bias, out, M, N, K, none, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// W8A8: plain int8 operands X [M, K], W [N, K] (K % 16 == 0) on the same
+// kernels (64 operand bytes per row and LDS block: 64 k), exact int32 acc.
+hipError_t gemm_i8_launch(const int8_t* X, const int8_t* W, const float* xs, const float* ws,
+                          const float* bias, void* out, int M, int N, int K, int epi, hipStream_t st) {
+    if (M == 0 || N == 0) return hipSuccess;
+    const LoraArgs none{nullptr, nullptr, 0, 0.0f};
+    switch (epi) {
+        case EPI_F32: return launch_epi<EPI_F32, false, true>(X, W, xs, ws, bias, out, M, N, K, none, st);
+        case EPI_BF16: return launch_epi<EPI_BF16, false, true>(X, W, xs, ws, bias, out, M, N, K, none, st);
+        case EPI_ACC: return launch_epi<EPI_ACC, false, true>(X, W, xs, ws, bias, out, M, N, K, none, st);
         default: return hipErrorInvalidValue;
     }
 }

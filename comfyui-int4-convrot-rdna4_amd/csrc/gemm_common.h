@@ -27,13 +27,15 @@ struct LoraArgs {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-// Accumulator of one output: the int8 kernels accumulate 256 * acc in int32
-// (operands are 16 * q), the bf6 kernels accumulate acc exactly in fp32
-// (integer products, |partial sums| < 2^24).
-__device__ __forceinline__ int acc_int(int v) { return v >> 8; }
-__device__ __forceinline__ int acc_int(float v) { return (int)v; }
-__device__ __forceinline__ float acc_float(int v) { return (float)(v >> 8); }
-__device__ __forceinline__ float acc_float(float v) { return v; }   // an exact integer already
+// Accumulator of one output: the int4-on-int8-MFMA kernels accumulate 256 * acc
+// in int32 (operands are 16 * q: ASH = 8), the W8A8 kernels acc itself (ASH =
+// 0; the float conversion of |acc| >= 2^24 rounds to nearest even, as the
+// reference's (float)acc does), the bf6 kernels acc exactly in fp32 (integer
+// products, |partial sums| < 2^24).
+template <int ASH> __device__ __forceinline__ int acc_int(int v) { return v >> ASH; }
+template <int ASH> __device__ __forceinline__ int acc_int(float v) { return (int)v; }
+template <int ASH> __device__ __forceinline__ float acc_float(int v) { return (float)(v >> ASH); }
+template <int ASH> __device__ __forceinline__ float acc_float(float v) { return v; }   // an exact integer already
 
 // Per-tile epilogue scales staged in LDS by the workgroup at kernel start:
 // xs of the tile's 256 rows, ws and bias of its 256 columns (0 outside M / N).
@@ -58,7 +60,7 @@ __device__ __forceinline__ void stage_scales(float* sc, const float* __restrict_
 // 32x32 layout: lane l, register r -> col = l % 32, row = 8 (r / 4) + 4 (l / 32) + r % 4.
 // The LoRA product uses the same layout (bf16 MFMA over R), issued by the
 // whole wave before any per-lane bounds check.
-template <int EPI, int FMT, int FNT, bool LORA, typename AccV>
+template <int EPI, int FMT, int FNT, bool LORA, int ASH = 8, typename AccV>
 __device__ __forceinline__ void epilogue_tiles(const AccV (&acc)[FMT][FNT], const float* __restrict__ xs,
                                                const float* __restrict__ ws, const float* __restrict__ bias,
                                                void* __restrict__ out, int M, int N, int row0, int col0,
@@ -98,7 +100,7 @@ __device__ __forceinline__ void epilogue_tiles(const AccV (&acc)[FMT][FNT], cons
             for (int r = 0; r < 16; ++r) {
                 const int row = rbase + 8 * (r >> 2) + (r & 3);
                 if (row >= M) continue;
-                const int a = acc_int(acc[i][j][r]);
+                const int a = acc_int<ASH>(acc[i][j][r]);
                 const size_t o = (size_t)row * N + col;
                 if constexpr (EPI == EPI_ACC) {
                     reinterpret_cast<int32_t*>(out)[o] = a;
@@ -139,7 +141,7 @@ __device__ __forceinline__ void epilogue_tiles(const AccV (&acc)[FMT][FNT], cons
 // finished, so the wave waits for L2 about once in all (more registers than
 // the other cases can spare).  The MFMA sequence (16-rank steps in ascending
 // order) is the same in every mode, so are the results.
-template <int EPI, int FMT, int FNT, int LR, int SCR_BYTES, typename AccV>
+template <int EPI, int FMT, int FNT, int LR, int SCR_BYTES, int ASH = 8, typename AccV>
 __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const float* sc,
                                              void* __restrict__ out, int M, int N, int tile_m0, int tile_n0,
                                              int row0, int col0, int lane, const LoraArgs& la, uint8_t* scr) {
@@ -234,13 +236,13 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
                 for (int q = 0; q < 4; ++q) {
                     uint8_t* dst = scr + (ii * 32 + l32) * RS + (j * 32 + 8 * q + 4 * h) * ES;
                     if constexpr (EPI == EPI_ACC) {
-                        *reinterpret_cast<int4*>(dst) = make_int4(acc_int(acc[i][j][4 * q]), acc_int(acc[i][j][4 * q + 1]),
-                                                                  acc_int(acc[i][j][4 * q + 2]), acc_int(acc[i][j][4 * q + 3]));
+                        *reinterpret_cast<int4*>(dst) = make_int4(acc_int<ASH>(acc[i][j][4 * q]), acc_int<ASH>(acc[i][j][4 * q + 1]),
+                                                                  acc_int<ASH>(acc[i][j][4 * q + 2]), acc_int<ASH>(acc[i][j][4 * q + 3]));
                     } else {
                         float v[4];
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            const float a = acc_float(acc[i][j][4 * q + e]);
+                            const float a = acc_float<ASH>(acc[i][j][4 * q + e]);
                             if constexpr (EPI == EPI_BF16_EAGER) {
                                 float t = bf16r(bf16r(a) * bf16r(xsv));
                                 t = bf16r(t * bf16r(wv[j][q][e]));

@@ -10,6 +10,10 @@
 // (_int4/eager.py:65-79 rotation, :104-120 quantizer, _int4/_codec.py:19-25
 // pack).  Nothing here follows the reference RDNA4 kernel
 // (_int4/int4_gemm.hip:348-408), whose fp32-reciprocal arithmetic differs.
+// The int8 tier (W8A8) uses the same kernels with 127 in place of 7, codes
+// clamped to [-127, 127] and stored as plain int8 (_int4/int8_eager.py:22-28;
+// again the eager arithmetic, not _int4/int4_gemm.hip:572-626, which keeps an
+// unrounded fp32 scale).
 //
 // Work layout
 //   * A lane owns a "chunk" of 16 consecutive elements (32 B of bf16, two
@@ -123,7 +127,7 @@ __device__ __forceinline__ int final_elem(int gl, int i) {
     else return i;
 }
 
-template <int DT, int G, int NPASS, bool STOCH>
+template <int DT, int G, int NPASS, bool STOCH, bool I8>
 __global__ __launch_bounds__(kMaxThreads) void rotquant_kernel(
         const void* __restrict__ x, const void* __restrict__ noise,
         int8_t* __restrict__ qout, float* __restrict__ sout,
@@ -200,7 +204,8 @@ __global__ __launch_bounds__(kMaxThreads) void rotquant_kernel(
 
     float a = __uint_as_float(row_ok ? rowmax[rloc] : 0u);
     a = fmaxf(a, clamp_floor<DT>());
-    const float s = round_to_dt<DT>(a / 7.0f);  // IEEE division (no fast-math)
+    constexpr float QMAX = I8 ? 127.0f : 7.0f;
+    const float s = round_to_dt<DT>(a / QMAX);  // IEEE division (no fast-math)
     if (row_ok && t == 0) sout[row] = s;
     const double rinv = 1.0 / (double)s;
     const float rinv32 = 1.0f / s;
@@ -228,10 +233,10 @@ __global__ __launch_bounds__(kMaxThreads) void rotquant_kernel(
             } else {
                 // f16 rows of zeros have s == 0 and give 0/0: the code is 0
                 if constexpr (DT == DT_F16) z = (z == z) ? z : 0.0f;
-                z = fminf(fmaxf(z, -7.0f), 7.0f);       // |z| <= 7.02 already; guards non-finite input
-                q = (int)__float_as_uint(z + kMagic);   // low nibble = rint_even(z)
+                z = fminf(fmaxf(z, -QMAX), QMAX);       // |z| <= QMAX (1 + 2^-9) already; guards non-finite input
+                q = (int)__float_as_uint(z + kMagic);   // low byte = rint_even(z)
             }
-            codes[i] = (uint8_t)(q & 0xF);
+            codes[i] = I8 ? (uint8_t)q : (uint8_t)(q & 0xF);
         }
         // scatter codes to their element positions, then read back own chunk
         __syncthreads();
@@ -242,7 +247,10 @@ __global__ __launch_bounds__(kMaxThreads) void rotquant_kernel(
             cb[(gfirst + e / kChunk) * 16 + (e % kChunk)] = codes[i];
         }
         __syncthreads();
-        if (ok) {
+        if (I8 && ok) {
+            *reinterpret_cast<uint4*>(qout + (size_t)row * K + (size_t)c * kChunk) =
+                reinterpret_cast<const uint4*>(cbuf)[tid];
+        } else if (ok) {
             const uint4 w = reinterpret_cast<const uint4*>(cbuf)[tid];
             const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
             uint32_t o[2];
@@ -375,9 +383,13 @@ __device__ __forceinline__ void b6_store_half(int8_t* out, int row, int K, int k
     }
 }
 
-// B6: write the codes in the B6T layout of the bf6 GEMM (b6t_layout.h) instead
-// of packed nibbles (K % 128 == 0; rows M .. ceil(M/256)*256 get zero codes).
-template <int DT, int G, int NPMAX, bool B6>
+// OUT selects the code format: OUT_PACK4 packed nibbles; OUT_B6T the B6T
+// layout of the bf6 GEMM (b6t_layout.h; K % 128 == 0; rows M .. ceil(M/256)*256
+// get zero codes); OUT_I8 the int8 tier's plain int8 codes (scale a / 127,
+// codes clamped to [-127, 127], _int4/int8_eager.py:22-28).
+enum : int { OUT_PACK4 = 0, OUT_B6T = 1, OUT_I8 = 2 };
+
+template <int DT, int G, int NPMAX, int OUT>
 __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
         const void* __restrict__ x, int8_t* __restrict__ qout, float* __restrict__ sout, int M, int K) {
     constexpr int LPG = G / kChunk;
@@ -394,6 +406,8 @@ __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
     const int gl = lane % LPG;
     const int gfirst = lane - gl;
     const float kMagic = 12582912.0f;
+    constexpr bool B6 = OUT == OUT_B6T;
+    constexpr float QMAX = OUT == OUT_I8 ? 127.0f : 7.0f;
 
     ChunkRegs<DT> nxt;
     int row = blockIdx.x * kWaves + wv;
@@ -461,7 +475,7 @@ __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
         for (int off = 32; off > 0; off >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, off));
         // bf16: lmax is a jammed value; its RNE is the max of the rounded values
         const float a = fmaxf(round_to_dt<DT>(lmax), clamp_floor<DT>());
-        const float s = round_to_dt<DT>(a / 7.0f);
+        const float s = round_to_dt<DT>(a / QMAX);
         if (lane == 0) sout[row] = s;
         const float rinv32 = 1.0f / s;
         const double rinv = 1.0 / (double)s;
@@ -475,12 +489,17 @@ __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
                 for (int i = 0; i < 16; i += 2) {
                     float z0, z1;
                     if constexpr (DT == DT_BF16) {
-                        // one packed RNE for both quotients; |z| <= 7.03 because
-                        // s >= bf16(absmax)/7 rounded, so rint stays in [-7, 7]
+                        // one packed RNE for both quotients; |z| <= QMAX (1 + 2^-9) because
+                        // s = RNE(absmax / QMAX), so rint stays in [-QMAX, QMAX]; the int8
+                        // clamp only guards non-finite input
                         const uint32_t zz = pack_bf16x2(bf16lo_to_f32(hv[p].w[i >> 1]) * rinv32,
                                                         bf16hi_to_f32(hv[p].w[i >> 1]) * rinv32);
                         z0 = bf16lo_to_f32(zz);
                         z1 = bf16hi_to_f32(zz);
+                        if constexpr (OUT == OUT_I8) {
+                            z0 = fminf(fmaxf(z0, -QMAX), QMAX);
+                            z1 = fminf(fmaxf(z1, -QMAX), QMAX);
+                        }
                     } else {
                         float zz[2];
 #pragma unroll
@@ -490,7 +509,7 @@ __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
                             if constexpr (DT == DT_F32) z = xv / s;
                             else z = round_to_dt<DT>((float)((double)xv * rinv));
                             if constexpr (DT == DT_F16) z = (z == z) ? z : 0.0f;
-                            zz[h] = fminf(fmaxf(z, -7.0f), 7.0f);
+                            zz[h] = fminf(fmaxf(z, -QMAX), QMAX);
                         }
                         z0 = zz[0];
                         z1 = zz[1];
@@ -503,7 +522,9 @@ __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
                 wave_sync();
                 const uint4 w = reinterpret_cast<const uint4*>(cb)[lane];
                 wave_sync();
-                if (B6 && ok) {
+                if (OUT == OUT_I8 && ok) {
+                    *reinterpret_cast<uint4*>(qout + (size_t)row * K + (size_t)c * kChunk) = w;
+                } else if (B6 && ok) {
                     // lane pair (2g', 2g'+1) holds the 32 codes of one MFMA group: the even
                     // lane its dwords 0..2, the odd lane dwords 3..5
                     const uint32_t c4[4] = {bf6_bytes(w.x), bf6_bytes(w.y), bf6_bytes(w.z), bf6_bytes(w.w)};
@@ -548,7 +569,7 @@ static int num_cus() {
     return g_num_cus;
 }
 
-template <int DT, int G, bool B6>
+template <int DT, int G, int OUT>
 static hipError_t rq_wave_launch(const void* x, int8_t* q, float* s, int M, int K, hipStream_t st) {
     const int np = (K / kChunk + 63) / 64;
     // enough waves to keep every CU busy; each wave then walks rows persistently
@@ -558,11 +579,11 @@ static hipError_t rq_wave_launch(const void* x, int8_t* q, float* s, int M, int 
     if (grid < 1) grid = 1;
     dim3 g(grid), b(64 * kWaves);
     if (np <= 3)
-        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 3, B6>), g, b, 0, st, x, q, s, M, K);
+        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 3, OUT>), g, b, 0, st, x, q, s, M, K);
     else if (np <= 6)
-        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 6, B6>), g, b, 0, st, x, q, s, M, K);
+        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 6, OUT>), g, b, 0, st, x, q, s, M, K);
     else
-        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 12, B6>), g, b, 0, st, x, q, s, M, K);
+        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 12, OUT>), g, b, 0, st, x, q, s, M, K);
     return hipGetLastError();
 }
 
@@ -591,17 +612,17 @@ static inline int rq_plan(int M, int K, int G, RQPlan* pl) {
     return 0;
 }
 
-template <int DT, int G, bool STOCH>
+template <int DT, int G, bool STOCH, bool I8 = false>
 static hipError_t rq_launch_g(const void* x, const void* noise, int8_t* q, float* s, int M, int K,
                               hipStream_t st) {
     if (M == 0) return hipSuccess;
-    if (!STOCH && K <= kWaveMaxK) return rq_wave_launch<DT, G, false>(x, q, s, M, K, st);
+    if (!STOCH && K <= kWaveMaxK) return rq_wave_launch<DT, G, I8 ? OUT_I8 : OUT_PACK4>(x, q, s, M, K, st);
     RQPlan pl;
     if (rq_plan(M, K, G, &pl) != 0) return hipErrorInvalidValue;
     dim3 grid(pl.grid), block(pl.block);
 #define RQ_CASE(NP)                                                                              \
     case NP:                                                                                     \
-        hipLaunchKernelGGL((rotquant_kernel<DT, G, NP, STOCH>), grid, block, 0, st, x, noise, q, s, \
+        hipLaunchKernelGGL((rotquant_kernel<DT, G, NP, STOCH, I8>), grid, block, 0, st, x, noise, q, s, \
                            M, K, pl.tpr, pl.rows_per_wg);                                        \
         break;
     switch (pl.npass) {
@@ -646,9 +667,9 @@ hipError_t rotquant_b6_launch(const void* x, int in_dtype, uint8_t* a6, float* s
     int8_t* q = reinterpret_cast<int8_t*>(a6);
 #define RB6_G(DT)                                                                                   \
     switch (G) {                                                                                    \
-        case 16: return rq_wave_launch<DT, 16, true>(x, q, s, M, K, st);                            \
-        case 64: return rq_wave_launch<DT, 64, true>(x, q, s, M, K, st);                            \
-        case 256: return rq_wave_launch<DT, 256, true>(x, q, s, M, K, st);                          \
+        case 16: return rq_wave_launch<DT, 16, OUT_B6T>(x, q, s, M, K, st);                         \
+        case 64: return rq_wave_launch<DT, 64, OUT_B6T>(x, q, s, M, K, st);                         \
+        case 256: return rq_wave_launch<DT, 256, OUT_B6T>(x, q, s, M, K, st);                       \
         default: return hipErrorInvalidValue;                                                       \
     }
     switch (in_dtype) {
@@ -661,5 +682,24 @@ hipError_t rotquant_b6_launch(const void* x, int in_dtype, uint8_t* a6, float* s
 }
 
 int rotquant_b6_max_k() { return kWaveMaxK; }
+
+// fused rotate + int8 quantize (W8A8 activations / weights): plain int8 [M, K]
+hipError_t rotquant_i8_launch(const void* x, int in_dtype, int8_t* q, float* s, int M, int K, int G,
+                              hipStream_t st) {
+#define RI8_G(DT)                                                                                   \
+    switch (G) {                                                                                    \
+        case 16: return rq_launch_g<DT, 16, false, true>(x, nullptr, q, s, M, K, st);               \
+        case 64: return rq_launch_g<DT, 64, false, true>(x, nullptr, q, s, M, K, st);               \
+        case 256: return rq_launch_g<DT, 256, false, true>(x, nullptr, q, s, M, K, st);             \
+        default: return hipErrorInvalidValue;                                                       \
+    }
+    switch (in_dtype) {
+        case DT_F32: RI8_G(DT_F32)
+        case DT_BF16: RI8_G(DT_BF16)
+        case DT_F16: RI8_G(DT_F16)
+        default: return hipErrorInvalidValue;
+    }
+#undef RI8_G
+}
 
 }  // namespace convrot

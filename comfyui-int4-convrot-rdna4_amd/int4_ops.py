@@ -357,13 +357,15 @@ if _COMFY_OPS and _CK_OK:
                     mode = self._quant_mode(prefix)
                     try:
                         if mode == "int8":
-                            raise NotImplementedError("ConvRot W8A8 has no gfx950 kernels in this build")
-                        stoch = (Int4ConvRotOps._STOCHASTIC_SEED
-                                 if Int4ConvRotOps.lora_mode == "Stochastic" else 0)
-                        qw, ws = _ck.quantize_convrot_w4a4_weight(
-                            w.to(dev, torch.float16), convrot_groupsize=gs, stochastic_rounding=stoch)
+                            from ._int4.int8_eager import quantize_convrot_w8a8_weight
+                            qw, ws = quantize_convrot_w8a8_weight(w.to(dev, torch.float16), convrot_groupsize=gs)
+                        else:
+                            stoch = (Int4ConvRotOps._STOCHASTIC_SEED
+                                     if Int4ConvRotOps.lora_mode == "Stochastic" else 0)
+                            qw, ws = _ck.quantize_convrot_w4a4_weight(
+                                w.to(dev, torch.float16), convrot_groupsize=gs, stochastic_rounding=stoch)
                         self._q, self._qs, self._qgs, self._qmode = qw, ws.float(), gs, mode
-                        self._q6 = _ck.prepare_convrot_w4a4_weight_bf6(qw)
+                        self._q6 = _ck.prepare_convrot_w4a4_weight_bf6(qw) if mode == "int4" else None
                         self.weight = None
                         state_dict.pop(wkey, None)
                         self._take_bias(state_dict, prefix, dev)

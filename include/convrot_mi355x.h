@@ -144,6 +144,35 @@ int cr_int4_convrot_gemm_bf6_lora(const void* A6, const void* W6, const void* xs
                                   const void* bias, const void* t, const void* U, int R, float scale,
                                   void* out, int M, int N, int K, int epilogue, void* stream);
 
+/*
+ * W8A8 tier (the reference's int8 ConvRot layers, _int4/int8_eager.py).
+ *
+ * Fused ConvRot rotation + rowwise int8 quantization:
+ *   qout     int8 [M, K]  plain codes in [-127, 127]
+ *   scaleout f32 [M]      per-row scale, an exact value of in_dtype
+ * G in {16, 64, 256}, K % G == 0, K <= 32768.  Arithmetic: the reference eager
+ * path (_int4/int8_eager.py:22-28 on _int4/eager.py:65-79): exactly rounded
+ * rotation, s = dt(fl32(absmax/127)), q = clamp(rint_even(dt(fl32(x/s))), +-127).
+ * Replaces: ck_convrot_quant_int8, reference _int4/int4_gemm.hip:664-676
+ * (bound at _int4/hip_loader.py:66-71, called at :95-113).
+ */
+int ck_convrot_quant_int8(const void* x, int in_dtype, void* qout, void* scaleout,
+                          int M, int K, int G, void* stream);
+
+/*
+ * W8A8 GEMM: out[m, n] = fl32(fl32(fl32(float(acc) * xscale[m]) * wscale[n]) + bias[n]),
+ * acc[m, n] = sum_k x[m, k] * w[n, k] exact in int32 (float(acc) rounds to
+ * nearest even once |acc| >= 2^24).  X int8 [M, K], W int8 [N, K], K % 16 == 0.
+ * Replaces: ck_int8_convrot_gemm, reference _int4/int4_gemm.hip:678-709
+ * (bound at _int4/hip_loader.py:63-65, called at :116-147).
+ */
+int ck_int8_convrot_gemm(const void* X, const void* W, const void* xscale, const void* wscale,
+                         const void* bias, void* out, int M, int N, int K, int out_dtype, void* stream);
+
+/* ck_int8_convrot_gemm with epilogue 0 (f32), 1 (bf16) or 3 (int32 accumulators). */
+int cr_int8_convrot_gemm_ex(const void* X, const void* W, const void* xscale, const void* wscale,
+                            const void* bias, void* out, int M, int N, int K, int epilogue, void* stream);
+
 /* Largest K accepted by the quantization entry points. */
 int cr_max_quant_k(void);
 

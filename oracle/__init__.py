@@ -22,6 +22,12 @@ Reference semantics followed (paths relative to the reference repository):
 * ``linear_eager``       -- ``_int4/eager.py:172-197``
 * ``quantize_weight``    -- ``_int4/eager.py:123-135`` (fp16 weights, as ``int4_ops.py:344-350``)
 * ``dequantize_weight``  -- ``_int4/eager.py:138-151``
+* ``quant_rows8``        -- ``_int4/int8_eager.py:22-28`` (W8A8 tier)
+* ``rotquant8``          -- ``_int4/int8_eager.py:81-83`` (activation) / ``:31-47`` (weight)
+* ``int8_gemm``          -- exact int32 accumulators of the W8A8 product
+  (``_int4/int4_gemm.hip:420-470``; the eager fp32 matmul of
+  ``_int4/int8_eager.py:86`` equals it while partial sums stay below 2^24)
+* ``linear_w8a8``        -- ``_int4/int8_eager.py:65-92`` with the exact product
 
 Parity pinning: every function is checked in ``tests/test_oracle.py`` against
 closed forms / brute force and against the golden vectors of ``tests/golden``.
@@ -60,6 +66,12 @@ def _load():
     lib.orc_rotquant.restype = i
     lib.orc_int_gemm.argtypes = [vp, vp, i, i, i, vp]
     lib.orc_int_gemm.restype = None
+    lib.orc_quant_rows8.argtypes = [vp, i, i, i, vp, vp]
+    lib.orc_quant_rows8.restype = None
+    lib.orc_rotquant8.argtypes = [vp, i, i, i, i, vp, vp, vp]
+    lib.orc_rotquant8.restype = i
+    lib.orc_int8_gemm.argtypes = [vp, vp, i, i, i, vp]
+    lib.orc_int8_gemm.restype = None
     lib.orc_epilogue_f32.argtypes = [vp, vp, vp, vp, i, i, i, vp, vp]
     lib.orc_epilogue_f32.restype = None
     lib.orc_epilogue_eager_bf16.argtypes = [vp, vp, vp, vp, i, i, vp]
@@ -283,3 +295,58 @@ def dequantize_weight(packed: np.ndarray, scales: np.ndarray, G: int) -> np.ndar
     H = hadamard(G).astype(np.float64)
     N, K = w.shape
     return (w.reshape(N, K // G, G) @ H.T).reshape(N, K)
+
+
+# ----------------------------------------------------------------------------
+# W8A8 tier
+# ----------------------------------------------------------------------------
+
+def quant_rows8(xr: np.ndarray, dt: int):
+    """Rowwise symmetric int8 quantization -> (codes int8 [M,K], scales f32 [M])."""
+    xr = _check(xr, dt)
+    M, K = xr.shape
+    q = np.empty((M, K), dtype=np.int8)
+    scales = np.empty((M,), dtype=np.float32)
+    _load().orc_quant_rows8(_p(xr), dt, M, K, _p(q), _p(scales))
+    return q, scales
+
+
+def rotquant8(x: np.ndarray, dt: int, G: int):
+    """Rotate + int8 quantize -> (codes int8 [M,K], scales f32 [M], xr)."""
+    x = _check(x, dt)
+    M, K = x.shape
+    if K % G:
+        raise ValueError(f"features {K} not divisible by group_size {G}")
+    q = np.empty((M, K), dtype=np.int8)
+    scales = np.empty((M,), dtype=np.float32)
+    xr = np.empty_like(x)
+    _load().orc_rotquant8(_p(x), dt, M, K, G, _p(q), _p(scales), _p(xr))
+    return q, scales, xr
+
+
+def int8_gemm(X: np.ndarray, W: np.ndarray) -> np.ndarray:
+    """Exact int32 accumulators acc[m, n] = sum_k x[m,k] w[n,k] of int8 operands."""
+    X = np.ascontiguousarray(X.view(np.int8))
+    W = np.ascontiguousarray(W.view(np.int8))
+    M, K = X.shape
+    N, K2 = W.shape
+    if K != K2:
+        raise ValueError(f"K mismatch: x {X.shape} w {W.shape}")
+    acc = np.empty((M, N), dtype=np.int32)
+    _load().orc_int8_gemm(_p(X), _p(W), M, N, K, _p(acc))
+    return acc
+
+
+def quantize_weight8(w: np.ndarray, dt: int, G: int):
+    """quantize_convrot_w8a8_weight semantics -> (int8 [N,K], scales f32 [N])."""
+    q, scales, _ = rotquant8(w, dt, G)
+    return q, scales
+
+
+def linear_w8a8(x, dt, qweight, wscales, bias=None, G=256, out_bf16=True):
+    """convrot_w8a8_linear (_int4/int8_eager.py:65-92) with the exact integer
+    product: rotate + int8 quantize x, exact int32 GEMM, fl32 epilogue, one RNE
+    to bf16 when out_bf16 (x bf16), else the f32 values."""
+    q, xs, _ = rotquant8(x, dt, G)
+    acc = int8_gemm(q, qweight)
+    return epilogue_f32(acc, xs, wscales, bias, out_bf16=out_bf16)

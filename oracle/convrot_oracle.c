@@ -396,6 +396,62 @@ int orc_rotquant(const void* x, int dt, int M, int K, int G, const void* noise,
 }
 
 /* ----------------------------------------------------------------------- */
+/* W8A8 tier: quantize_signed_int8_rowwise (_int4/int8_eager.py:22-28)     */
+/*   a = max(max_k |xr|, dt(1e-10));  s = RNE_dt(fl32(a / 127))            */
+/*   q = clamp(rint_even(RNE_dt(fl32(xr / s))), -127, 127)                 */
+/* stored as plain int8 [M, K] (_int4/int8_eager.py:31-47).  A NaN quotient */
+/* (0/0 for an f16 row of zeros) gives code 0.                             */
+/* ----------------------------------------------------------------------- */
+
+void orc_quant_rows8(const void* xr, int dt, int M, int K, int8_t* q8, float* scales) {
+    float lo = clamp_floor_value(dt);
+    for (int m = 0; m < M; ++m) {
+        size_t base = (size_t)m * K;
+        float a = 0.0f;
+        for (int k = 0; k < K; ++k) {
+            float v = fabsf(load_val(xr, dt, base + k));
+            if (v > a) a = v;
+        }
+        if (a < lo) a = lo;
+        float s = orc_round_to(a / 127.0f, dt);
+        scales[m] = s;
+        for (int k = 0; k < K; ++k) {
+            float t = orc_round_to(load_val(xr, dt, base + k) / s, dt);
+            float r = nearbyintf(t);               /* ties to even */
+            int c = 0;
+            if (!isnan(r)) c = r < -127.0f ? -127 : (r > 127.0f ? 127 : (int)r);
+            q8[base + k] = (int8_t)c;
+        }
+    }
+}
+
+/* convrot_w8a8_linear's activation half / quantize_convrot_w8a8_weight     */
+/* (_int4/int8_eager.py:31-47, 81-83): rotate then quantize to int8.        */
+int orc_rotquant8(const void* x, int dt, int M, int K, int G, int8_t* q8, float* scales,
+                  void* xr_out /* nullable */) {
+    size_t esz = dt == DT_F32 ? 4 : 2;
+    void* xr = xr_out ? xr_out : malloc((size_t)M * K * esz);
+    int n = orc_rotate(x, dt, M, K, G, xr);
+    orc_quant_rows8(xr, dt, M, K, q8, scales);
+    if (!xr_out) free(xr);
+    return n;
+}
+
+/* W8A8 accumulators acc[m,n] = sum_k x[m,k] * w[n,k], exact in int64 and    */
+/* returned as int32 (|acc| <= 127^2 K < 2^31 for K < 133000).              */
+void orc_int8_gemm(const int8_t* X, const int8_t* W, int M, int N, int K, int32_t* acc) {
+    for (int m = 0; m < M; ++m) {
+        const int8_t* a = X + (size_t)m * K;
+        for (int n = 0; n < N; ++n) {
+            const int8_t* b = W + (size_t)n * K;
+            int64_t s = 0;
+            for (int k = 0; k < K; ++k) s += (int32_t)a[k] * b[k];
+            acc[(size_t)m * N + n] = (int32_t)s;
+        }
+    }
+}
+
+/* ----------------------------------------------------------------------- */
 /* a7 unpack (_int4/_codec.py:28-36) and a8 int GEMM (_int4/eager.py:160-162) */
 /* ----------------------------------------------------------------------- */
 
@@ -433,6 +489,10 @@ void orc_int_gemm(const int8_t* Xp, const int8_t* Wp, int M, int N, int K, int32
 /* fp32 chain: o = fl32(fl32(fl32(acc*xs)*ws) + b).  For out_dtype f32 this is
  * the eager int4_linear computation exactly (_int4/eager.py:164-168 with
  * out_dtype f32: the integer matmul is exact in f32 because |acc| < 2^24).
+ * For the W8A8 tier it is the reference kernel's epilogue
+ * ((float)acc * xscale * ws + bias, _int4/int4_gemm.hip:555-558) and the eager
+ * one (_int4/int8_eager.py:87-91) whenever its fp32 matmul is exact
+ * (|partial sums| < 2^24); (float)acc rounds to nearest even above that.
  * out_bf16 != 0 rounds the final value once to bf16 (bits in out16). */
 void orc_epilogue_f32(const int32_t* acc, const float* xs, const float* ws, const float* bias,
                       int M, int N, int out_bf16, float* out32, uint16_t* out16) {

@@ -122,6 +122,60 @@ def edge_cases() -> dict:
     return cases
 
 
+def tie_rows8(K: int = 256) -> torch.Tensor:
+    """bf16 rows for the int8 quantizer itself (already-rotated values):
+    half-integer quotients (ties to even) and scales that are not powers of
+    two.  (No input reaches the clamp: s = RNE(a/127) is within 2^-9 of a/127,
+    so every quotient rounds to at most 127.)"""
+    rows = []
+    v = np.zeros(K)                        # absmax 127 -> s = 1
+    v[0] = 127.0
+    ties = [0.5, 1.5, 2.5, 3.5, 64.5, 125.5, 126.5]
+    for i, t in enumerate(ties):
+        v[1 + 2 * i] = t
+        v[2 + 2 * i] = -t
+    rows.append(v)
+    v = np.zeros(K)                        # absmax 127.5 -> s = bf16(127.5/127) = 1.0078125: 127.5/s = 126.5 ties to 126
+    v[3] = 127.5
+    v[4] = -127.5
+    v[5] = 63.5
+    rows.append(v)
+    v = np.zeros(K)                        # absmax 254 -> s = 2: ties at odd integers
+    v[7] = -254.0
+    for i, t in enumerate([1.0, 3.0, 5.0, 7.0, 251.0, 253.0]):
+        v[10 + i] = t
+        v[20 + i] = -t
+    rows.append(v)
+    rs = np.random.RandomState(17)         # generic scale (absmax 100)
+    v = rs.uniform(-100.0, 100.0, K)
+    v[0] = 100.0
+    rows.append(v)
+    return torch.from_numpy(np.stack(rows).astype(np.float32)).to(torch.bfloat16)
+
+
+def clamp_rows8() -> torch.Tensor:
+    """bf16 x [2, 16] (G = 16) whose exact rotation is +-127.5 e_0, the largest
+    bf16 absmax below 128: s = bf16(127.5/127) = 1.0078125 and the quotient
+    127.5/s = 126.5 is a tie that rounds to 126."""
+    v = np.zeros((2, 16))
+    v[0, 0] = 127.5
+    v[1, 0] = -127.5
+    x = preimage_rows(v, 16)
+    xt = torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16)
+    if not np.array_equal(xt.float().numpy().astype(np.float64), x):
+        raise AssertionError("preimage not representable in bf16")
+    return xt
+
+
+def small_w8a8_case():
+    """x bf16 [64, 512], W fp16 [96, 512] ~ N(0, 0.02), bias fp16 [96]: K small
+    enough that every fp32 partial sum of the int8 product is exact (< 2^24)."""
+    x = outlier_activations(64, 512, seed=21)
+    w = normal_weight(96, 512, seed=22)
+    b = normal_bias(96, seed=23)
+    return x, w, b
+
+
 def stochastic_weight_case() -> torch.Tensor:
     return normal_weight(64, 512, seed=11)
 

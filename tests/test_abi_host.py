@@ -25,6 +25,9 @@ def test_header_declares_reference_entry_points():
     # names a binding of the reference's ctypes loader resolves (hip_loader.py:50-61)
     assert "ck_convrot_quant_int4" in syms
     assert "ck_int4_convrot_gemm" in syms
+    # the int8 tier's pair (hip_loader.py:63-71)
+    assert "ck_convrot_quant_int8" in syms
+    assert "ck_int8_convrot_gemm" in syms
 
 
 def test_library_exports_every_declared_symbol(native):
@@ -39,7 +42,7 @@ def test_library_exports_every_declared_symbol(native):
 
 def test_library_queries_without_gpu(native):
     lib = native.load_library()
-    assert lib.cr_abi_version() == 2
+    assert lib.cr_abi_version() == 3
     assert lib.cr_max_quant_k() == 32768
     assert lib.cr_max_quant_bf6_k() == 12288
 
@@ -69,6 +72,12 @@ def test_argument_errors_return_minus_one(native):
     assert lib.cr_int4_to_bf6(n, n, 4, 96, n) == -1                           # K % 128
     assert lib.cr_int4_convrot_gemm_bf6(n, n, n, n, n, n, 4, 4, 192, 0, n) == -1
     assert lib.cr_int4_convrot_gemm_bf6(n, n, n, n, n, n, 4, 4, 256, 4, n) == -1
+    assert lib.ck_convrot_quant_int8(n, 1, n, n, 4, 256, 32, n) == -1      # bad G
+    assert lib.ck_convrot_quant_int8(n, 1, n, n, 4, 100, 16, n) == -1      # K % G
+    assert lib.ck_convrot_quant_int8(n, 3, n, n, 4, 256, 256, n) == -1     # bad dtype
+    assert lib.ck_int8_convrot_gemm(n, n, n, n, n, n, 4, 4, 40, 1, n) == -1  # K % 16
+    assert lib.ck_int8_convrot_gemm(n, n, n, n, n, n, 4, 4, 64, 2, n) == -1  # out dtype
+    assert lib.cr_int8_convrot_gemm_ex(n, n, n, n, n, n, 4, 4, 64, 2, n) == -1  # no eager bf16 chain for int8
 
 
 def test_pick_groupsize(backend):

@@ -6,8 +6,8 @@ import numpy as np
 import pytest
 import torch
 
-from inputs import (bf16_bits, config1_bias, config1_weight, config1_x, edge_cases,
-                    hadamard_np, small_linear_case, stochastic_weight_case)
+from inputs import (bf16_bits, clamp_rows8, config1_bias, config1_weight, config1_x, edge_cases,
+                    hadamard_np, small_linear_case, small_w8a8_case, stochastic_weight_case, tie_rows8)
 
 DT_OF = {torch.bfloat16: 1, torch.float16: 2, torch.float32: 0}
 
@@ -256,3 +256,101 @@ def test_eager_chain_vs_torch_ops(oracle):
     t = t * torch.from_numpy(ws).reshape(1, -1).to(torch.bfloat16)
     t = t + torch.from_numpy(b).to(torch.bfloat16).reshape(1, -1)
     assert np.array_equal(oracle.epilogue_eager_bf16(acc, xs, ws, b), np_of(t))
+
+
+# ----------------------------------------------------------------------------
+# W8A8 tier (int8_eager.py)
+# ----------------------------------------------------------------------------
+
+def test_golden_int8_config1(oracle, goldens):
+    q, s, _ = oracle.rotquant8(bf16_bits(config1_x()), oracle.BF16, 256)
+    assert np.array_equal(q[:32], goldens["i8_c1_q_rows32"])
+    assert sha(q) == str(goldens["i8_c1_q_sha"])
+    assert np.array_equal(s, goldens["i8_c1_s"])
+    qw, ws = oracle.quantize_weight8(np_of(config1_weight()), oracle.F16, 256)
+    assert np.array_equal(qw[:64], goldens["i8_c1_qw_rows64"])
+    assert sha(qw) == str(goldens["i8_c1_qw_sha"])
+    assert np.array_equal(ws, goldens["i8_c1_wscale"])
+
+
+@pytest.mark.parametrize("name", list(edge_cases().keys()))
+def test_golden_int8_edge_cases(oracle, goldens, name):
+    xe, G = edge_cases()[name]
+    dt = DT_OF[xe.dtype]
+    q, s, xr = oracle.rotquant8(np_of(xe), dt, G)
+    if dt == oracle.F32:
+        # torch's fp32 rotation is not correctly rounded (the absmax element may
+        # differ in its last bits), so compare the quantizer on torch's own xr
+        xr_t = torch.from_numpy(goldens[f"edge_{name}_xr"])
+        q, s = oracle.quant_rows8(np_of(xr_t), dt)
+    assert np.array_equal(q, goldens[f"i8_edge_{name}_q"])
+    assert np.array_equal(s, goldens[f"i8_edge_{name}_s"])
+
+
+def test_golden_int8_ties_and_largest_quotient(oracle, goldens):
+    q, s = oracle.quant_rows8(np_of(tie_rows8()), oracle.BF16)
+    assert np.array_equal(q, goldens["i8_ties_q"]) and np.array_equal(s, goldens["i8_ties_s"])
+    q, s, _ = oracle.rotquant8(np_of(clamp_rows8()), oracle.BF16, 16)
+    assert np.array_equal(q, goldens["i8_maxq_q"]) and np.array_equal(s, goldens["i8_maxq_s"])
+    assert q[0, 0] == 126 and q[1, 0] == -126 and s[0] == 1.0078125
+
+
+def test_golden_int8_linear(oracle, goldens):
+    """K = 512: the eager fp32 matmul of int8 codes is exact, so the eager
+    output equals the exact-product epilogue bit for bit."""
+    x, w, b = small_w8a8_case()
+    qw, ws = oracle.quantize_weight8(np_of(w), oracle.F16, 256)
+    assert np.array_equal(qw, goldens["i8_lin_qw"]) and np.array_equal(ws, goldens["i8_lin_ws"])
+    y = oracle.linear_w8a8(np_of(x), oracle.BF16, qw, ws, b.float().numpy(), 256)
+    assert np.array_equal(y, goldens["i8_lin_y"])
+
+
+def test_int8_quantizer_brute_force_small(oracle):
+    """Codes from the eager formula by hand (explicit bf16 roundings, numpy's
+    half-to-even round), independent of the oracle's code."""
+    rs = np.random.RandomState(12)
+    for trial in range(20):
+        row = oracle.f32_to_bf16((rs.standard_normal(32) * (0.01 + 3 * trial)).astype(np.float32))
+        q, s = oracle.quant_rows8(row.reshape(1, 32), oracle.BF16)
+        vals = oracle.bf16_to_f32(row).astype(np.float64)
+        a = max(np.abs(vals).max(), _bf16(1e-10))
+        sc = _bf16(np.float32(a) / np.float32(127.0))
+        assert s[0] == sc
+        for k in range(32):
+            t = _bf16(np.float32(vals[k]) / np.float32(sc))
+            assert q[0, k] == int(np.clip(np.round(t), -127, 127))
+
+
+def test_int8_quantizer_properties(oracle):
+    """Every code within half a step (plus the bf16 quotient rounding) of
+    xr / s; the absmax element at +-126 or +-127 (a / s lies in [126.5, 127.25]
+    since s = RNE(a / 127) is within 2^-8 of a / 127); odd symmetry; codes in
+    [-127, 127]."""
+    rs = np.random.RandomState(13)
+    x = oracle.f32_to_bf16((rs.standard_t(3, size=(64, 512)) * 2).astype(np.float32))
+    q, s = oracle.quant_rows8(x, oracle.BF16)
+    v = oracle.bf16_to_f32(x).astype(np.float64)
+    z = v / s[:, None].astype(np.float64)
+    assert np.all(np.abs(q - z) <= 0.5 + np.abs(z) * 2.0 ** -8)
+    qmax = np.abs(q.astype(np.int32)).max(axis=1)
+    assert np.all(qmax >= 126) and qmax.max() <= 127 and (qmax == 127).any()
+    qn, sn = oracle.quant_rows8(x ^ np.uint16(0x8000), oracle.BF16)
+    assert np.array_equal(qn, -q) and np.array_equal(sn, s)
+
+
+def test_int8_zero_rows(oracle):
+    q, s = oracle.quant_rows8(np.zeros((1, 16), dtype=np.uint16), oracle.BF16)
+    assert s[0] == _bf16(np.float32(_bf16(1e-10)) / np.float32(127.0)) and not q.any()
+    q, s = oracle.quant_rows8(np.zeros((1, 16), dtype=np.uint16), oracle.F16)
+    assert s[0] == 0.0 and not q.any()
+
+
+def test_int8_gemm_matches_numpy(oracle):
+    rs = np.random.RandomState(14)
+    X = rs.randint(-128, 128, size=(9, 4096)).astype(np.int8)
+    W = rs.randint(-128, 128, size=(7, 4096)).astype(np.int8)
+    W[0] = -128
+    X[0] = -128                                   # |acc| = 2^26: beyond fp32's exact integers
+    acc = oracle.int8_gemm(X, W)
+    assert np.array_equal(acc, X.astype(np.int64) @ W.astype(np.int64).T)
+    assert acc[0, 0] == 128 * 128 * 4096
