@@ -370,13 +370,19 @@ def bench_dit(args):
                                                            vp(xs.data_ptr()), M, K, m._qgs, sptr)))
             calls.append(("lora_down", lib.cr_lora_down, (vp(x.data_ptr()), 1, vp(D.data_ptr()), vp(t.data_ptr()),
                                                           M, K, R, sptr)))
-            calls.append(("gemm_lora", lib.cr_int4_convrot_gemm_bf6_lora,
+            # the GEMM as the Linear runs it: k-split when the library chooses one
+            ns = lib.cr_gemm_bf6_choose_nsplit(M, N, K)
+            nb = lib.cr_gemm_bf6_splitk_workspace(M, N, ns)
+            wsp = torch.empty((max(nb, 16),), dtype=torch.uint8, device="cuda")
+            keep.append(wsp)
+            calls.append(("gemm_lora", lib.cr_int4_convrot_gemm_bf6_splitk,
                           (vp(a6.data_ptr()), vp(m._q6.data_ptr()), vp(xs.data_ptr()), vp(m._qs.data_ptr()),
                            vp(b32.data_ptr()), vp(t.data_ptr()), vp(U.data_ptr()), R, ctypes.c_float(1.0),
-                           vp(out.data_ptr()), M, N, K, 1, sptr)))
-            calls.append(("gemm_plain", lib.cr_int4_convrot_gemm_bf6,
+                           vp(out.data_ptr()), M, N, K, 1, ns, vp(wsp.data_ptr()), nb, sptr)))
+            calls.append(("gemm_plain", lib.cr_int4_convrot_gemm_bf6_splitk,
                           (vp(a6.data_ptr()), vp(m._q6.data_ptr()), vp(xs.data_ptr()), vp(m._qs.data_ptr()),
-                           vp(b32.data_ptr()), vp(out.data_ptr()), M, N, K, 1, sptr)))
+                           vp(b32.data_ptr()), None, None, 0, ctypes.c_float(0.0),
+                           vp(out.data_ptr()), M, N, K, 1, ns, vp(wsp.data_ptr()), nb, sptr)))
         kern = {}
         reps = 3
         for rep in range(reps + 1):

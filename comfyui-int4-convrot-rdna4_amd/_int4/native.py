@@ -44,6 +44,10 @@ _SIGNATURES = {
     "ck_convrot_quant_int8": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
     "ck_int8_convrot_gemm": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
     "cr_int8_convrot_gemm_ex": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
+    "cr_gemm_bf6_choose_nsplit": ([_i, _i, _i], _i),
+    "cr_gemm_bf6_splitk_workspace": ([_i, _i, _i], ctypes.c_size_t),
+    "cr_int4_convrot_gemm_bf6_splitk": ([_vp] * 7 + [_i, ctypes.c_float, _vp] + [_i] * 5 + [_vp, ctypes.c_size_t, _vp],
+                                        _i),
     "cr_max_quant_k": ([], _i),
     "cr_abi_version": ([], _i),
 }
@@ -338,29 +342,58 @@ def _bf6_gemm_args(a6, w6, x_scale, w_scale, bias, M, N):
     return _aligned(a6), _aligned(w6), xs, wsc, b, M, N, K
 
 
-def int4_convrot_gemm_bf6(a6, w6, x_scale, w_scale, bias, epilogue: int, M=None, N=None):
-    """W4A4 GEMM on B6T operands (exact accumulators), epilogue 0..3 as
-    int4_convrot_gemm_ex.  M / N default to the scale lengths."""
+def choose_nsplit_bf6(M: int, N: int, K: int) -> int:
+    """The library's k-split count for an M x N x K bf6 GEMM (1: no split)."""
+    return int(load_library().cr_gemm_bf6_choose_nsplit(M, N, K))
+
+
+def _bf6_launch(a6, w6, xs, wsc, b, t, up, R, scale, out, M, N, K, epilogue, nsplit):
+    """One bf6 GEMM: unsplit through the plain entry points, split-K through
+    cr_int4_convrot_gemm_bf6_splitk with a workspace from torch's allocator."""
     lib = load_library()
+    if nsplit is None:
+        nsplit = lib.cr_gemm_bf6_choose_nsplit(M, N, K) if M > 0 and N > 0 else 1
+    st = _stream(a6.device)
+    if nsplit <= 1:
+        if t is None:
+            rc = lib.cr_int4_convrot_gemm_bf6(_ptr(a6), _ptr(w6), _ptr(xs), _ptr(wsc), _ptr(b), _ptr(out),
+                                              M, N, K, epilogue, st)
+            name = "cr_int4_convrot_gemm_bf6"
+        else:
+            rc = lib.cr_int4_convrot_gemm_bf6_lora(_ptr(a6), _ptr(w6), _ptr(xs), _ptr(wsc), _ptr(b), _ptr(t),
+                                                   _ptr(up), R, ctypes.c_float(scale), _ptr(out), M, N, K,
+                                                   epilogue, st)
+            name = "cr_int4_convrot_gemm_bf6_lora"
+    else:
+        nbytes = lib.cr_gemm_bf6_splitk_workspace(M, N, nsplit)
+        ws = torch.empty((nbytes,), dtype=torch.uint8, device=a6.device)
+        rc = lib.cr_int4_convrot_gemm_bf6_splitk(_ptr(a6), _ptr(w6), _ptr(xs), _ptr(wsc), _ptr(b), _ptr(t),
+                                                 _ptr(up), R, ctypes.c_float(scale), _ptr(out), M, N, K, epilogue,
+                                                 nsplit, _ptr(ws), nbytes, st)
+        name = "cr_int4_convrot_gemm_bf6_splitk"
+    if rc != 0:
+        raise RuntimeError(f"{name} failed, hipError={rc}")
+    return out
+
+
+def int4_convrot_gemm_bf6(a6, w6, x_scale, w_scale, bias, epilogue: int, M=None, N=None, nsplit=None):
+    """W4A4 GEMM on B6T operands (exact accumulators), epilogue 0..3 as
+    int4_convrot_gemm_ex.  M / N default to the scale lengths.  nsplit: k
+    splits (None: the library's choice; the outputs are identical either way)."""
     a6, w6, xs, wsc, b, M, N, K = _bf6_gemm_args(a6, w6, x_scale, w_scale, bias, M, N)
     odt = {EPI_F32: torch.float32, EPI_BF16: torch.bfloat16, EPI_BF16_EAGER: torch.bfloat16,
            EPI_ACC: torch.int32}[epilogue]
     out = torch.empty((M, N), dtype=odt, device=a6.device)
-    rc = lib.cr_int4_convrot_gemm_bf6(_ptr(a6), _ptr(w6), _ptr(xs), _ptr(wsc), _ptr(b), _ptr(out),
-                                      M, N, K, epilogue, _stream(a6.device))
-    if rc != 0:
-        raise RuntimeError(f"cr_int4_convrot_gemm_bf6 failed, hipError={rc}")
-    return out
+    return _bf6_launch(a6, w6, xs, wsc, b, None, None, 0, 0.0, out, M, N, K, epilogue, nsplit)
 
 
-def int4_gemm_acc_bf6(a6, w6, M: int, N: int):
+def int4_gemm_acc_bf6(a6, w6, M: int, N: int, nsplit=None):
     """int32 accumulators of the bf6 GEMM (exact)."""
-    return int4_convrot_gemm_bf6(a6, w6, None, None, None, EPI_ACC, M=M, N=N)
+    return int4_convrot_gemm_bf6(a6, w6, None, None, None, EPI_ACC, M=M, N=N, nsplit=nsplit)
 
 
-def int4_convrot_gemm_bf6_lora(a6, w6, x_scale, w_scale, bias, t, up, scale: float, epilogue: int):
+def int4_convrot_gemm_bf6_lora(a6, w6, x_scale, w_scale, bias, t, up, scale: float, epilogue: int, nsplit=None):
     """int4_convrot_gemm_bf6 + scale * (t @ up^T) in the epilogue (0..2)."""
-    lib = load_library()
     a6, w6, xs, wsc, b, M, N, K = _bf6_gemm_args(a6, w6, x_scale, w_scale, bias, None, None)
     _check_cuda(t, up)
     t = _aligned(t)
@@ -370,12 +403,7 @@ def int4_convrot_gemm_bf6_lora(a6, w6, x_scale, w_scale, bias, t, up, scale: flo
         raise ValueError("lora operands: t [M, R] and up [N, R] bf16")
     odt = {EPI_F32: torch.float32, EPI_BF16: torch.bfloat16, EPI_BF16_EAGER: torch.bfloat16}[epilogue]
     out = torch.empty((M, N), dtype=odt, device=a6.device)
-    rc = lib.cr_int4_convrot_gemm_bf6_lora(_ptr(a6), _ptr(w6), _ptr(xs), _ptr(wsc), _ptr(b), _ptr(t), _ptr(up),
-                                           R, ctypes.c_float(scale), _ptr(out), M, N, K, epilogue,
-                                           _stream(a6.device))
-    if rc != 0:
-        raise RuntimeError(f"cr_int4_convrot_gemm_bf6_lora failed, hipError={rc}")
-    return out
+    return _bf6_launch(a6, w6, xs, wsc, b, t, up, R, scale, out, M, N, K, epilogue, nsplit)
 
 
 # ----------------------------------------------------------------------------

@@ -25,7 +25,9 @@ hipError_t gemm_i8_launch(const int8_t* X, const int8_t* W, const float* xs, con
                           const float* bias, void* out, int M, int N, int K, int epi, hipStream_t st);
 hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, const float* ws, const float* bias,
                            const void* t, const void* U, int R, float scale, void* out, int M, int N, int K,
-                           int epi, hipStream_t st);
+                           int epi, int nsplit, void* workspace, hipStream_t st);
+int gemm_bf6_choose_nsplit(int M, int N, int K);
+size_t gemm_bf6_splitk_workspace(int M, int N, int nsplit);
 }  // namespace convrot
 
 #define API extern "C" __attribute__((visibility("default")))
@@ -119,7 +121,7 @@ API int cr_int4_convrot_gemm_bf6(const void* A6, const void* W6, const void* xsc
     return (int)convrot::gemm_bf6_launch(A6, W6, reinterpret_cast<const float*>(xscale),
                                          reinterpret_cast<const float*>(wscale),
                                          reinterpret_cast<const float*>(bias), nullptr, nullptr, 0, 0.0f, out,
-                                         M, N, K, epilogue, reinterpret_cast<hipStream_t>(stream));
+                                         M, N, K, epilogue, 1, nullptr, reinterpret_cast<hipStream_t>(stream));
 }
 
 API int cr_int4_convrot_gemm_bf6_lora(const void* A6, const void* W6, const void* xscale, const void* wscale,
@@ -130,7 +132,33 @@ API int cr_int4_convrot_gemm_bf6_lora(const void* A6, const void* W6, const void
     return (int)convrot::gemm_bf6_launch(A6, W6, reinterpret_cast<const float*>(xscale),
                                          reinterpret_cast<const float*>(wscale),
                                          reinterpret_cast<const float*>(bias), t, U, R, scale, out, M, N, K,
-                                         epilogue, reinterpret_cast<hipStream_t>(stream));
+                                         epilogue, 1, nullptr, reinterpret_cast<hipStream_t>(stream));
+}
+
+API int cr_gemm_bf6_choose_nsplit(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || !bf6_k_ok(K)) return 1;
+    return convrot::gemm_bf6_choose_nsplit(M, N, K);
+}
+
+API size_t cr_gemm_bf6_splitk_workspace(int M, int N, int nsplit) {
+    if (M <= 0 || N <= 0 || nsplit < 1) return 0;
+    return convrot::gemm_bf6_splitk_workspace(M, N, nsplit);
+}
+
+API int cr_int4_convrot_gemm_bf6_splitk(const void* A6, const void* W6, const void* xscale, const void* wscale,
+                                        const void* bias, const void* t, const void* U, int R, float scale,
+                                        void* out, int M, int N, int K, int epilogue, int nsplit,
+                                        void* workspace, size_t workspace_bytes, void* stream) {
+    if (!bf6_k_ok(K) || M < 0 || N < 0 || nsplit < 1 || nsplit > K / 128) return -1;
+    if (t != nullptr && (epilogue < 0 || epilogue > 2 || !lora_rank_ok(R) || U == nullptr)) return -1;
+    if (t == nullptr && (epilogue < 0 || epilogue > 3)) return -1;
+    if (nsplit > 1 && M > 0 && N > 0 &&
+        (workspace == nullptr || workspace_bytes < convrot::gemm_bf6_splitk_workspace(M, N, nsplit)))
+        return -1;
+    return (int)convrot::gemm_bf6_launch(A6, W6, reinterpret_cast<const float*>(xscale),
+                                         reinterpret_cast<const float*>(wscale),
+                                         reinterpret_cast<const float*>(bias), t, U, R, scale, out, M, N, K,
+                                         epilogue, nsplit, workspace, reinterpret_cast<hipStream_t>(stream));
 }
 
 API int ck_convrot_quant_int8(const void* x, int in_dtype, void* qout, void* scaleout,
@@ -159,4 +187,4 @@ API int ck_int8_convrot_gemm(const void* X, const void* W, const void* xscale, c
 
 API int cr_max_quant_k(void) { return convrot::rotquant_max_k(); }
 
-API int cr_abi_version(void) { return 3; }
+API int cr_abi_version(void) { return 4; }

@@ -114,30 +114,50 @@ __device__ __forceinline__ v8i bf6_operand_odd(uint4 q, uint4 p) {
     return (v8i){(int)q.z, (int)q.w, (int)p.x, (int)p.y, (int)p.z, (int)p.w, 0, 0};
 }
 
-template <int EPI, int LR>
+// SPLIT: split-K partial kernel.  Workgroup b takes tile b % T and the 128-k
+// blocks [s nkb / S, (s + 1) nkb / S) of split s = b / T (T tiles, S splits),
+// and stores its raw accumulators (exact integers in fp32) in the workspace in
+// register order, 32 KB per wave: part[((s T + tile) 8 + wave) * 8192 +
+// (q * 64 + lane) * 4 + e] = acc[q / 8][(q / 4) % 2][4 (q % 4) + e].  The
+// scales, the epilogue and the LoRA term run once per output, in the reduce
+// kernel below.
+template <int EPI, int LR, bool SPLIT>
 __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
         const uint8_t* __restrict__ A6, const uint8_t* __restrict__ W6,
         const float* __restrict__ xs, const float* __restrict__ ws, const float* __restrict__ bias,
-        void* __restrict__ out, int M, int N, int K, LoraArgs lora, int gm) {
+        void* __restrict__ out, int M, int N, int K, LoraArgs lora, int gm, int nsplit,
+        float* __restrict__ part) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds6[];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave >> 2, wn = wave & 3;
-    int tm, tn;
-    tile_of_block(blockIdx.x, (M + B6_BM - 1) / B6_BM, (N + B6_BN - 1) / B6_BN, gm, tm, tn);
+    const int tiles_m = (M + B6_BM - 1) / B6_BM, tiles_n = (N + B6_BN - 1) / B6_BN;
+    const int nkb_all = K / 128;
+    int tm, tn, kb0 = 0, nkb = nkb_all, split = 0, tile = 0;
+    if constexpr (SPLIT) {
+        const int T = tiles_m * tiles_n;
+        split = blockIdx.x / T;
+        tile = blockIdx.x - split * T;
+        tm = tile % tiles_m;
+        tn = tile / tiles_m;
+        kb0 = (int)((long long)split * nkb_all / nsplit);
+        nkb = (int)((long long)(split + 1) * nkb_all / nsplit) - kb0;
+    } else {
+        tile_of_block(blockIdx.x, tiles_m, tiles_n, gm, tm, tn);
+    }
     const int m0 = tm * B6_BM;
     const int n0 = tn * B6_BN;
-    const int nkb = K / 128;
 
     float* sc = reinterpret_cast<float*>(lds6 + B6_RING_BYTES);
-    stage_scales(sc, xs, ws, bias, M, N, m0, n0, tid, B6_THREADS);   // visible after the loop's first barrier
+    if constexpr (!SPLIT)
+        stage_scales(sc, xs, ws, bias, M, N, m0, n0, tid, B6_THREADS);   // visible after the loop's first barrier
 
     // waves 0..3 copy the A chunk of a block, waves 4..7 the B chunk (6 KB each)
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    const uint8_t* my_chunks = wave_u < 4 ? A6 + (size_t)(m0 / B6_BM) * nkb * B6_CHUNK
-                                          : W6 + (size_t)(n0 / B6_BN) * nkb * B6_CHUNK;
+    const uint8_t* my_chunks = (wave_u < 4 ? A6 + (size_t)tm * nkb_all * B6_CHUNK
+                                           : W6 + (size_t)tn * nkb_all * B6_CHUNK) + (size_t)kb0 * B6_CHUNK;
     const uint8_t* my_src = my_chunks + (wave_u & 3) * (B6_LOADS * 1024) + lane * 16;
     const uint32_t my_lds = (uint32_t)(uintptr_t)lds6 + wave_u * (B6_LOADS * 1024);
     v16f acc[4][2];
@@ -234,6 +254,17 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));                 // the copies past the end have landed
 
+    if constexpr (SPLIT) {
+        float4* dst = reinterpret_cast<float4*>(part) +
+                      ((size_t)(split * tiles_m * tiles_n + tile) * 8 + wave) * 2048 + lane;
+#pragma unroll
+        for (int q = 0; q < 32; ++q) {
+            const v16f& a = acc[q >> 3][(q >> 2) & 1];
+            const int r = 4 * (q & 3);
+            dst[q * 64] = make_float4(a[r], a[r + 1], a[r + 2], a[r + 3]);
+        }
+        return;
+    }
     __syncthreads();                                     // every wave is done with the stages
     // keep the epilogue's index arithmetic out of the main loop's registers
     int em0 = m0, en0 = n0, elane = lane;
@@ -243,25 +274,88 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
                                        en0 + wn * 64, elane, lora, lds6 + wave * SCR);
 }
 
+// Split-K reduce: one 256-lane workgroup per (tile, wave slot) of the main
+// kernel; its wave v takes the slot's 32-row tile v.  A wave sums the S
+// partials of its 32 x 64 piece in split order (exact: integers below 2^24)
+// into the main kernel's accumulator layout and runs the same epilogue code on
+// it, so every output equals the unsplit kernel's bit for bit.
+constexpr int B6R_WAVES = 4;
+constexpr int B6R_SCR = 32 * (2 * 32 * 4 + 16);        // one 32-row f32 pass of the epilogue scratch
+
+template <int EPI, int LR>
+__global__ __launch_bounds__(64 * B6R_WAVES) void w4a4_bf6_splitk_reduce_kernel(
+        const float* __restrict__ part, int nsplit, const float* __restrict__ xs, const float* __restrict__ ws,
+        const float* __restrict__ bias, void* __restrict__ out, int M, int N, LoraArgs lora) {
+    __shared__ __attribute__((aligned(16))) float sc[EPI_SCALE_FLOATS];
+    __shared__ __attribute__((aligned(16))) uint8_t scr[B6R_WAVES][B6R_SCR];
+    const int lane = threadIdx.x & 63;
+    const int v = threadIdx.x >> 6;                      // row tile of the slot
+    const int tiles_m = (M + B6_BM - 1) / B6_BM, tiles_n = (N + B6_BN - 1) / B6_BN;
+    const int T = tiles_m * tiles_n;
+    const int tile = blockIdx.x >> 3, w = blockIdx.x & 7;
+    const int tm = tile % tiles_m, tn = tile / tiles_m;
+    const int m0 = tm * B6_BM, n0 = tn * B6_BN;
+    const int wm = w >> 2, wn = w & 3;
+    stage_scales(sc, xs, ws, bias, M, N, m0, n0, threadIdx.x, 64 * B6R_WAVES);
+    v16f acc[1][2];
+    acc[0][0] = (v16f){0};
+    acc[0][1] = (v16f){0};
+    for (int s = 0; s < nsplit; ++s) {
+        const float4* src = reinterpret_cast<const float4*>(part) + ((size_t)(s * T + tile) * 8 + w) * 2048 +
+                            (size_t)v * 8 * 64 + lane;
+        float4 q4[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) q4[q] = src[q * 64];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            v16f& a = acc[0][q >> 2];
+            const int r = 4 * (q & 3);
+            a[r] += q4[q].x; a[r + 1] += q4[q].y; a[r + 2] += q4[q].z; a[r + 3] += q4[q].w;
+        }
+    }
+    __syncthreads();                                     // staged scales visible
+    epilogue_lds<EPI, 1, 2, LR, B6R_SCR>(acc, sc, out, M, N, m0, n0, m0 + wm * 128 + v * 32, n0 + wn * 64,
+                                         lane, lora, scr[v]);
+}
+
 template <int EPI, int LR>
 static hipError_t launch_bf6(const uint8_t* A6, const uint8_t* W6, const float* xs, const float* ws,
                              const float* bias, void* out, int M, int N, int K, const LoraArgs& la,
-                             hipStream_t st) {
+                             int nsplit, float* part, hipStream_t st) {
     constexpr int kMaxDev = 64;
     static bool attr_set[kMaxDev] = {};
+    static bool attr_split[kMaxDev] = {};
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= kMaxDev) return hipErrorInvalidDevice;
-    if (!attr_set[dev]) {
-        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_bf6_kernel<EPI, LR>),
+    const int tiles_m = (M + B6_BM - 1) / B6_BM;
+    const int ntiles = tiles_m * ((N + B6_BN - 1) / B6_BN);
+    if (nsplit <= 1) {
+        if (!attr_set[dev]) {
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_bf6_kernel<EPI, LR, false>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, B6_LDS_BYTES);
+            if (e != hipSuccess) return e;
+            attr_set[dev] = true;
+        }
+        hipLaunchKernelGGL((w4a4_gemm_bf6_kernel<EPI, LR, false>), dim3(ntiles), dim3(B6_THREADS), B6_LDS_BYTES,
+                           st, A6, W6, xs, ws, bias, out, M, N, K, la, tile_group_rows(tiles_m), 1, nullptr);
+        return hipGetLastError();
+    }
+    // the partial kernel is the same for every epilogue and LoRA rank
+    if (!attr_split[dev]) {
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_bf6_kernel<EPI_ACC, 0, true>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, B6_LDS_BYTES);
         if (e != hipSuccess) return e;
-        attr_set[dev] = true;
+        attr_split[dev] = true;
     }
-    const int ntiles = ((M + B6_BM - 1) / B6_BM) * ((N + B6_BN - 1) / B6_BN);
-    hipLaunchKernelGGL((w4a4_gemm_bf6_kernel<EPI, LR>), dim3(ntiles), dim3(B6_THREADS), B6_LDS_BYTES, st,
-                       A6, W6, xs, ws, bias, out, M, N, K, la, tile_group_rows((M + B6_BM - 1) / B6_BM));
+    const LoraArgs none{nullptr, nullptr, 0, 0.0f};
+    hipLaunchKernelGGL((w4a4_gemm_bf6_kernel<EPI_ACC, 0, true>), dim3(ntiles * nsplit), dim3(B6_THREADS),
+                       B6_LDS_BYTES, st, A6, W6, nullptr, nullptr, nullptr, nullptr, M, N, K, none, 1, nsplit, part);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((w4a4_bf6_splitk_reduce_kernel<EPI, LR>), dim3(ntiles * 8), dim3(64 * B6R_WAVES), 0, st,
+                       part, nsplit, xs, ws, bias, out, M, N, la);
     return hipGetLastError();
 }
 
@@ -275,17 +369,18 @@ hipError_t int4_to_bf6_launch(const void* src, void* dst, int rows, int K, hipSt
 
 hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, const float* ws, const float* bias,
                            const void* t, const void* U, int R, float scale, void* out, int M, int N, int K,
-                           int epi, hipStream_t st) {
+                           int epi, int nsplit, void* workspace, hipStream_t st) {
+    float* part = reinterpret_cast<float*>(workspace);
     if (M == 0 || N == 0) return hipSuccess;
     const uint8_t* a = reinterpret_cast<const uint8_t*>(A6);
     const uint8_t* w = reinterpret_cast<const uint8_t*>(W6);
     if (t == nullptr) {
         const LoraArgs none{nullptr, nullptr, 0, 0.0f};
         switch (epi) {
-            case EPI_F32: return launch_bf6<EPI_F32, 0>(a, w, xs, ws, bias, out, M, N, K, none, st);
-            case EPI_BF16: return launch_bf6<EPI_BF16, 0>(a, w, xs, ws, bias, out, M, N, K, none, st);
-            case EPI_BF16_EAGER: return launch_bf6<EPI_BF16_EAGER, 0>(a, w, xs, ws, bias, out, M, N, K, none, st);
-            case EPI_ACC: return launch_bf6<EPI_ACC, 0>(a, w, xs, ws, bias, out, M, N, K, none, st);
+            case EPI_F32: return launch_bf6<EPI_F32, 0>(a, w, xs, ws, bias, out, M, N, K, none, nsplit, part, st);
+            case EPI_BF16: return launch_bf6<EPI_BF16, 0>(a, w, xs, ws, bias, out, M, N, K, none, nsplit, part, st);
+            case EPI_BF16_EAGER: return launch_bf6<EPI_BF16_EAGER, 0>(a, w, xs, ws, bias, out, M, N, K, none, nsplit, part, st);
+            case EPI_ACC: return launch_bf6<EPI_ACC, 0>(a, w, xs, ws, bias, out, M, N, K, none, nsplit, part, st);
             default: return hipErrorInvalidValue;
         }
     }
@@ -294,9 +389,9 @@ hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, cons
 #define BF6_LORA_CASE(LRV)                                                                                      \
     case LRV:                                                                                                   \
         switch (epi) {                                                                                          \
-            case EPI_F32: return launch_bf6<EPI_F32, LRV>(a, w, xs, ws, bias, out, M, N, K, la, st);            \
-            case EPI_BF16: return launch_bf6<EPI_BF16, LRV>(a, w, xs, ws, bias, out, M, N, K, la, st);          \
-            case EPI_BF16_EAGER: return launch_bf6<EPI_BF16_EAGER, LRV>(a, w, xs, ws, bias, out, M, N, K, la, st); \
+            case EPI_F32: return launch_bf6<EPI_F32, LRV>(a, w, xs, ws, bias, out, M, N, K, la, nsplit, part, st);            \
+            case EPI_BF16: return launch_bf6<EPI_BF16, LRV>(a, w, xs, ws, bias, out, M, N, K, la, nsplit, part, st);          \
+            case EPI_BF16_EAGER: return launch_bf6<EPI_BF16_EAGER, LRV>(a, w, xs, ws, bias, out, M, N, K, la, nsplit, part, st); \
             default: return hipErrorInvalidValue;                                                               \
         }
     switch (R / 32) {
@@ -304,6 +399,36 @@ hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, cons
         default: return hipErrorInvalidValue;
     }
 #undef BF6_LORA_CASE
+}
+
+// Number of k splits for an M x N x K product (1: no split).  Cost model,
+// fitted to kernel traces of M = 512 .. 2048 and K = 3072 .. 12288: a launch
+// runs in waves of 256 workgroups (one per CU); a workgroup costs 0.82 us per
+// 128-k block plus 2.5 us; a split adds the reduce kernel, 3.1 us plus 0.09 us
+// per (tile, split) partial (256 KB written and read back).  A split must win
+// by 8% to be taken.
+int gemm_bf6_choose_nsplit(int M, int N, int K) {
+    const int tiles = ((M + B6_BM - 1) / B6_BM) * ((N + B6_BN - 1) / B6_BN);
+    const int nkb = K / 128;
+    auto cost = [&](int s) {
+        const double waves = (double)((tiles * s + 255) / 256);
+        double c = waves * ((double)nkb / s * 0.82 + 2.5);
+        if (s > 1) c += 3.1 + 0.09 * s * tiles;
+        return c;
+    };
+    int best = 1;
+    const double c1 = cost(1);
+    double bc = c1;
+    for (int s = 2; s <= 16 && s <= nkb / 2; ++s) {
+        const double c = cost(s);
+        if (c < bc) { bc = c; best = s; }
+    }
+    return bc < 0.92 * c1 ? best : 1;
+}
+
+size_t gemm_bf6_splitk_workspace(int M, int N, int nsplit) {
+    const size_t tiles = (size_t)((M + B6_BM - 1) / B6_BM) * ((N + B6_BN - 1) / B6_BN);
+    return nsplit <= 1 ? 0 : (size_t)nsplit * tiles * 8 * 8192 * sizeof(float);
 }
 
 }  // namespace convrot

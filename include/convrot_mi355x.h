@@ -19,6 +19,8 @@
 #ifndef CONVROT_MI355X_H
 #define CONVROT_MI355X_H
 
+#include <stddef.h>
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -143,6 +145,32 @@ int cr_int4_convrot_gemm_bf6(const void* A6, const void* W6, const void* xscale,
 int cr_int4_convrot_gemm_bf6_lora(const void* A6, const void* W6, const void* xscale, const void* wscale,
                                   const void* bias, const void* t, const void* U, int R, float scale,
                                   void* out, int M, int N, int K, int epilogue, void* stream);
+
+/*
+ * Split-K form of the bf6 GEMM for small tile grids (few rows, large K): S
+ * workgroups per 256 x 256 output tile each take 1/S of the 128-k blocks and
+ * store their raw accumulators (exact integers) in `workspace`; a second kernel
+ * sums the S partials in a fixed order and runs the same epilogue code, so the
+ * outputs are bit-identical to cr_int4_convrot_gemm_bf6 / _lora for every S.
+ *   t == NULL: no LoRA term, epilogue 0..3; else LoRA as cr_int4_convrot_gemm_bf6_lora
+ *   (epilogue 0..2).  1 <= nsplit <= K / 128; nsplit == 1 needs no workspace,
+ *   otherwise workspace_bytes >= cr_gemm_bf6_splitk_workspace(M, N, nsplit).
+ * Replaces: ck_int4_convrot_gemm_splitk, reference _int4/int4_gemm.hip:634-645
+ * (chosen by _choose_nsplit, _int4/hip_loader.py:20-36, called at :176-190),
+ * which adds rounded fp32 partials into a zeroed [M, N] buffer with atomics and
+ * leaves bias and cast to torch; this one owns its workspace layout and
+ * finishes the epilogue itself.
+ */
+int cr_int4_convrot_gemm_bf6_splitk(const void* A6, const void* W6, const void* xscale, const void* wscale,
+                                    const void* bias, const void* t, const void* U, int R, float scale,
+                                    void* out, int M, int N, int K, int epilogue, int nsplit,
+                                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* The library's k-split count for an M x N x K bf6 GEMM (1 = no split). */
+int cr_gemm_bf6_choose_nsplit(int M, int N, int K);
+
+/* Workspace bytes of cr_int4_convrot_gemm_bf6_splitk: nsplit * tiles * 256 KB (0 when nsplit == 1). */
+size_t cr_gemm_bf6_splitk_workspace(int M, int N, int nsplit);
 
 /*
  * W8A8 tier (the reference's int8 ConvRot layers, _int4/int8_eager.py).

@@ -17,7 +17,7 @@ from fake_comfy import install_fake_comfy
 
 def header_symbols():
     text = open(os.path.join(ROOT, "include", "convrot_mi355x.h")).read()
-    return re.findall(r"^\s*int\s+(\w+)\s*\(", text, flags=re.M)
+    return re.findall(r"^\s*(?:int|size_t)\s+(\w+)\s*\(", text, flags=re.M)
 
 
 def test_header_declares_reference_entry_points():
@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(native):
 
 def test_library_queries_without_gpu(native):
     lib = native.load_library()
-    assert lib.cr_abi_version() == 3
+    assert lib.cr_abi_version() == 4
     assert lib.cr_max_quant_k() == 32768
     assert lib.cr_max_quant_bf6_k() == 12288
 
@@ -78,6 +78,13 @@ def test_argument_errors_return_minus_one(native):
     assert lib.ck_int8_convrot_gemm(n, n, n, n, n, n, 4, 4, 40, 1, n) == -1  # K % 16
     assert lib.ck_int8_convrot_gemm(n, n, n, n, n, n, 4, 4, 64, 2, n) == -1  # out dtype
     assert lib.cr_int8_convrot_gemm_ex(n, n, n, n, n, n, 4, 4, 64, 2, n) == -1  # no eager bf16 chain for int8
+    sk = lib.cr_int4_convrot_gemm_bf6_splitk
+    assert sk(n, n, n, n, n, n, n, 0, f, n, 4, 4, 256, 0, 0, n, 0, n) == -1        # nsplit < 1
+    assert sk(n, n, n, n, n, n, n, 0, f, n, 4, 4, 256, 0, 3, n, 1 << 30, n) == -1  # more splits than 128-k blocks
+    assert sk(n, n, n, n, n, n, n, 0, f, n, 4, 4, 256, 0, 2, n, 1 << 30, n) == -1  # no workspace
+    ws_need = lib.cr_gemm_bf6_splitk_workspace(4, 4, 2)
+    assert sk(n, n, n, n, n, n, n, 0, f, n, 4, 4, 256, 0, 2, ctypes.c_void_p(16), ws_need - 1, n) == -1
+    assert sk(n, n, n, n, n, ctypes.c_void_p(16), n, 32, f, n, 4, 4, 256, 3, 1, n, 0, n) == -1  # acc dump with LoRA
 
 
 def test_pick_groupsize(backend):
@@ -198,3 +205,17 @@ def test_ops_refuses_unknown_prequant_layout(ops_mod):
     lin = ops_mod.Int4ConvRotOps.Linear(3072, 32, bias=False)
     sd = {"weight": torch.zeros(32, 100, dtype=torch.int8), "weight_scale": torch.ones(32)}
     assert lin._load_prequantized(dict(sd), "", "weight", "weight_scale", sd["weight"]) is False
+
+
+def test_split_choice_and_workspace(native):
+    """The k-split choice is host arithmetic: large tile grids never split,
+    small-M / large-K products do, within 2 .. nkb; the workspace is S * tiles
+    * 256 KB."""
+    lib = native.load_library()
+    assert lib.cr_gemm_bf6_choose_nsplit(4608, 3072, 3072) == 1
+    assert lib.cr_gemm_bf6_choose_nsplit(4608, 12288, 3072) == 1
+    s = lib.cr_gemm_bf6_choose_nsplit(512, 3072, 12288)
+    assert 2 <= s <= 96
+    assert lib.cr_gemm_bf6_choose_nsplit(256, 256, 256) <= 2
+    assert lib.cr_gemm_bf6_splitk_workspace(512, 3072, 4) == 4 * 24 * 256 * 256 * 4
+    assert lib.cr_gemm_bf6_splitk_workspace(300, 300, 1) == 0

@@ -1,0 +1,80 @@
+"""GPU parity of the split-K bf6 GEMM: for every split count the accumulators
+equal the oracle's and every epilogue (with and without the LoRA term) is
+bit-identical to the unsplit kernel's, on full and ragged tile grids."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def cu(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def operands(native, M, N, K, seed):
+    rs = np.random.RandomState(seed)
+    xp = rs.randint(-128, 128, size=(M, K // 2)).astype(np.int8)
+    wp = rs.randint(-128, 128, size=(N, K // 2)).astype(np.int8)
+    xs = rs.uniform(0.005, 0.05, size=M).astype(np.float32)
+    ws = rs.uniform(0.005, 0.05, size=N).astype(np.float32)
+    b = (rs.standard_normal(N) * 0.01).astype(np.float32)
+    return xp, wp, native.int4_to_bf6(cu(xp)), native.int4_to_bf6(cu(wp)), cu(xs), cu(ws), cu(b)
+
+
+SPLIT_CASES = [(512, 3072, 12288, [2, 5, 6, 16, 96]), (300, 700, 1024, [2, 3, 8]), (1024, 3072, 3072, [2, 4, 24]),
+               (64, 256, 256, [2]), (257, 513, 3840, [7, 30])]
+
+
+@pytest.mark.parametrize("M,N,K,splits", SPLIT_CASES)
+def test_splitk_acc_exact(native, oracle, gpu, M, N, K, splits):
+    print(f"splitk acc M={M} N={N} K={K}", flush=True)
+    xp, wp, a6, w6, *_ = operands(native, M, N, K, M + N + K)
+    base = native.int4_gemm_acc_bf6(a6, w6, M, N, nsplit=1)
+    rows = np.arange(M) if M <= 300 else np.random.RandomState(2).choice(M, 24, replace=False)
+    assert np.array_equal(base.cpu().numpy()[rows], oracle.int_gemm(xp[rows], wp))
+    for s in splits:
+        acc = native.int4_gemm_acc_bf6(a6, w6, M, N, nsplit=s)
+        assert torch.equal(acc, base), s
+
+
+@pytest.mark.parametrize("M,N,K,splits", SPLIT_CASES[:3])
+def test_splitk_epilogues_identical(native, gpu, M, N, K, splits):
+    _, _, a6, w6, xs, ws, b = operands(native, M, N, K, 7 * M + K)
+    for epi in (native.EPI_F32, native.EPI_BF16, native.EPI_BF16_EAGER):
+        for bias in (b, None):
+            base = native.int4_convrot_gemm_bf6(a6, w6, xs, ws, bias, epi, nsplit=1)
+            for s in splits:
+                out = native.int4_convrot_gemm_bf6(a6, w6, xs, ws, bias, epi, nsplit=s)
+                assert torch.equal(out.view(torch.int16) if out.dtype == torch.bfloat16 else out.view(torch.int32),
+                                   base.view(torch.int16) if base.dtype == torch.bfloat16 else base.view(torch.int32)), (epi, s)
+
+
+@pytest.mark.parametrize("R", [32, 64, 128])
+def test_splitk_lora_identical(native, gpu, R):
+    M, N, K = 512, 3072, 12288
+    _, _, a6, w6, xs, ws, b = operands(native, M, N, K, R)
+    g = torch.Generator(device="cuda").manual_seed(R)
+    t = torch.randn((M, R), generator=g, device="cuda").to(torch.bfloat16)
+    U = (torch.randn((N, R), generator=g, device="cuda") * 0.1).to(torch.bfloat16)
+    for epi in (native.EPI_F32, native.EPI_BF16):
+        base = native.int4_convrot_gemm_bf6_lora(a6, w6, xs, ws, b, t, U, 0.75, epi, nsplit=1)
+        for s in (3, 8):
+            out = native.int4_convrot_gemm_bf6_lora(a6, w6, xs, ws, b, t, U, 0.75, epi, nsplit=s)
+            assert torch.equal(out, base), (epi, s)
+
+
+def test_auto_split_linear_matches_unsplit(backend, native, gpu):
+    """convrot_w4a4_linear at a small-M shape (where the library splits) is
+    bit-identical to the same product forced unsplit."""
+    from inputs import normal_bias, normal_weight, outlier_activations
+    M, N, K = 512, 3072, 12288
+    assert native.choose_nsplit_bf6(M, N, K) > 1
+    x = outlier_activations(M, K, seed=3).cuda()
+    qw, ws = backend.quantize_convrot_w4a4_weight(normal_weight(N, K, seed=4).cuda())
+    b = normal_bias(N, seed=5).cuda()
+    y = backend.convrot_w4a4_linear(x, qw, ws, bias=b)
+    a6, xs = native.convrot_quant_bf6(x, 256)
+    y1 = native.int4_convrot_gemm_bf6(a6, backend.prepare_convrot_w4a4_weight_bf6(qw), xs, ws, b,
+                                      native.EPI_BF16, nsplit=1)
+    assert torch.equal(y, y1)
