@@ -104,9 +104,10 @@ def main():
                          "W8A8 tier (int8 activations and weights on int8 MFMA)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (counter calibration)")
-    ap.add_argument("--workload", choices=("block-linears", "dit8"), default="block-linears",
+    ap.add_argument("--workload", choices=("block-linears", "dit8", "gemm-sweep"), default="block-linears",
                     help="block-linears: the four linears of one DiT block (the headline line); "
-                         "dit8: the synthetic 8-block double-stream DiT stack through Int4ConvRotOps")
+                         "dit8: the synthetic 8-block double-stream DiT stack through Int4ConvRotOps; "
+                         "gemm-sweep: the W4A4 GEMM alone over a token sweep (k-split as the Linear chooses)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -115,6 +116,9 @@ def main():
         sys.exit(2)
     if args.workload == "dit8":
         bench_dit(args)
+        return
+    if args.workload == "gemm-sweep":
+        bench_gemm_sweep(args)
         return
 
     import torch
@@ -269,6 +273,82 @@ def main():
     }
     if copy_cal:
         line["copy_calibration"] = copy_cal
+    print(json.dumps(line), flush=True)
+
+
+SWEEP_M = (512, 1024, 2048, 4608, 8192, 16384)
+SWEEP_KN = ((3072, 3072), (3072, 12288), (12288, 3072), (3840, 15360))
+
+
+def bench_gemm_sweep(args):
+    """The W4A4 GEMM alone (bf6 operands, bf16 output with bias) over the token
+    sweep M x (K, N): int4 codes uniform in [-8, 7], scales U(0.005, 0.05),
+    bias N(0, 0.01), seed 0; each shape timed over `--steps` launches with HIP
+    events on the launch stream, k-split as the Linear replacement chooses it."""
+    import numpy as np
+    import torch
+    importlib.import_module("comfyui-int4-convrot-rdna4_amd")
+    native = importlib.import_module("comfyui-int4-convrot-rdna4_amd._int4.native")
+    if not native.is_available():
+        raise SystemExit("libconvrot_gfx950.so is not loadable on a gfx950 device; nothing to measure")
+    lib = native.load_library()
+    stream = torch.cuda.current_stream()
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+    vp = ctypes.c_void_p
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    detail, total_ops, total_s = {}, 0.0, 0.0
+    for (K, N) in SWEEP_KN:
+        w6 = native.int4_to_bf6(torch.randint(-128, 128, (N, K // 2), generator=g, device="cuda",
+                                              dtype=torch.int8))
+        ws = torch.rand(N, generator=g, device="cuda") * 0.045 + 0.005
+        b = torch.randn(N, generator=g, device="cuda") * 0.01
+        for M in SWEEP_M:
+            a6 = native.int4_to_bf6(torch.randint(-128, 128, (M, K // 2), generator=g, device="cuda",
+                                                  dtype=torch.int8))
+            xs = torch.rand(M, generator=g, device="cuda") * 0.045 + 0.005
+            out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+            ns = lib.cr_gemm_bf6_choose_nsplit(M, N, K)
+            nb = lib.cr_gemm_bf6_splitk_workspace(M, N, ns)
+            wsp = torch.empty((max(nb, 16),), dtype=torch.uint8, device="cuda")
+            call = (vp(a6.data_ptr()), vp(w6.data_ptr()), vp(xs.data_ptr()), vp(ws.data_ptr()), vp(b.data_ptr()),
+                    None, None, 0, ctypes.c_float(0.0), vp(out.data_ptr()), M, N, K, 1, ns, vp(wsp.data_ptr()),
+                    nb, sptr)
+            for _ in range(args.warmup):
+                assert lib.cr_int4_convrot_gemm_bf6_splitk(*call) == 0
+            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(args.steps)]
+            torch.cuda.synchronize()
+            for e0, e1 in evs:
+                e0.record(stream)
+                assert lib.cr_int4_convrot_gemm_bf6_splitk(*call) == 0
+                e1.record(stream)
+            torch.cuda.synchronize()
+            us = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in evs)
+            med = us[len(us) // 2]
+            ops = 2.0 * M * N * K
+            detail[f"{M}x{K}->{N}"] = {"us": round(med, 2), "TOPS": round(ops / med / 1e6, 1), "nsplit": ns}
+            total_ops += ops
+            total_s += med * 1e-6
+            del a6, out, wsp
+    line = {
+        "metric": "W4A4 GEMM token sweep: effective int4 TOPS (%int8 MFMA peak)",
+        "value": round(total_ops / total_s / 1e12, 1),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(total_s * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "W4A4 GEMM token sweep, bf6 operands, bf16 out + bias: M in %s x (K, N) in %s; codes "
+                               "uniform [-8, 7], scales U(0.005, 0.05)" % (list(SWEEP_M), [list(x) for x in SWEEP_KN])},
+        "pct_int8_peak": round(100 * total_ops / total_s / 1e12 / PEAK_INT8_TOPS, 2),
+        "detail": detail,
+    }
     print(json.dumps(line), flush=True)
 
 
