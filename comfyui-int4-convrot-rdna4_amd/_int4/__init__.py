@@ -220,6 +220,29 @@ def convrot_w4a4_linear(
     out_dtype = x.dtype if x.dtype in _NATIVE_OUT else torch.float32
     epi = native.EPI_BF16 if out_dtype == torch.bfloat16 else native.EPI_F32
     K, N = x2d.shape[1], qweight.shape[0]
+    if bf6_path_ok(K) and x2d.is_cuda and (lora is None or x2d.dtype in (torch.bfloat16, torch.float16)):
+        # the whole linear in one library call (same kernels, same bits as the steps below)
+        w6 = qweight_bf6 if qweight_bf6 is not None else prepare_convrot_w4a4_weight_bf6(qweight)
+        if w6.shape != (native.bf6_rows(N), K // 4 * 3):
+            raise ValueError(f"qweight_bf6 of shape {tuple(w6.shape)} does not encode a [{N}, {K}] weight")
+        wsc = wscales if wscales.dtype == torch.float32 and wscales.is_contiguous() else \
+            wscales.reshape(-1).to(torch.float32).contiguous()
+        # the bias is read as stored (f32 / bf16 / f16): no conversion launch per call
+        b32 = None if bias is None else (bias.reshape(-1) if bias.dtype in native._IN_DTYPE_CODE else
+                                         bias.reshape(-1).to(torch.float32))
+        if b32 is not None and not b32.is_contiguous():
+            b32 = b32.contiguous()
+        down = up = None
+        if lora is not None:
+            down, up = lora
+            if down.shape[1] != K or up.shape[0] != N or up.shape[1] != down.shape[0]:
+                raise ValueError(f"LoRA shapes D {tuple(down.shape)} U {tuple(up.shape)} do not fit K={K} N={N}")
+        native._check_cuda(x2d, w6, wsc, b32, down, up)
+        out = native.convrot_w4a4_linear_bf6(native._aligned(x2d), w6, wsc, b32, down, up, 1.0, epi,
+                                             convrot_groupsize, N)
+        if out.dtype != x.dtype:
+            out = out.to(x.dtype)
+        return out.reshape(*orig_shape[:-1], N)
     t = up = None
     if lora is not None:
         down, up = lora

@@ -48,6 +48,9 @@ _SIGNATURES = {
     "cr_gemm_bf6_splitk_workspace": ([_i, _i, _i], ctypes.c_size_t),
     "cr_int4_convrot_gemm_bf6_splitk": ([_vp] * 7 + [_i, ctypes.c_float, _vp] + [_i] * 5 + [_vp, ctypes.c_size_t, _vp],
                                         _i),
+    "cr_convrot_w4a4_linear_bf6": ([_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _i, ctypes.c_float, _vp] + [_i] * 5
+                                   + [_vp, ctypes.c_size_t, _vp], _i),
+    "cr_convrot_w4a4_linear_bf6_workspace": ([_i, _i, _i, _i], ctypes.c_size_t),
     "cr_max_quant_k": ([], _i),
     "cr_abi_version": ([], _i),
 }
@@ -466,3 +469,25 @@ def int8_convrot_gemm(x_int8, w_int8, x_scale, w_scale, bias, out_dtype):
         raise ValueError(f"int8 gemm output dtype must be float32/bfloat16, got {out_dtype}")
     return int8_convrot_gemm_ex(x_int8, w_int8, x_scale, w_scale, bias,
                                 EPI_F32 if out_dtype == torch.float32 else EPI_BF16)
+
+
+def convrot_w4a4_linear_bf6(x2d, w6, w_scale, bias, down, up, scale: float, epilogue: int, convrot_groupsize: int,
+                            N: int):
+    """The whole bf6 linear in one library call (cr_convrot_w4a4_linear_bf6):
+    rotate + quantize x2d [M, K], the LoRA down projection when ``down`` is given,
+    the GEMM with the epilogue (and the LoRA term).  w_scale f32 [N]; bias [N]
+    f32 / bf16 / f16 as stored, or None; down [R, K] / up [N, R] bf16."""
+    lib = load_library()
+    M, K = x2d.shape
+    odt = {EPI_F32: torch.float32, EPI_BF16: torch.bfloat16, EPI_BF16_EAGER: torch.bfloat16}[epilogue]
+    out = torch.empty((M, N), dtype=odt, device=x2d.device)
+    R = 0 if down is None else down.shape[0]
+    nbytes = lib.cr_convrot_w4a4_linear_bf6_workspace(M, N, K, R)
+    ws = torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=x2d.device)
+    bdt = 0 if bias is None else _IN_DTYPE_CODE[bias.dtype]
+    rc = lib.cr_convrot_w4a4_linear_bf6(_ptr(x2d), _IN_DTYPE_CODE[x2d.dtype], _ptr(w6), _ptr(w_scale), _ptr(bias),
+                                        bdt, _ptr(down), _ptr(up), R, ctypes.c_float(scale), _ptr(out), epilogue,
+                                        M, N, K, convrot_groupsize, _ptr(ws), nbytes, _stream(x2d.device))
+    if rc != 0:
+        raise RuntimeError(f"cr_convrot_w4a4_linear_bf6 failed, hipError={rc}")
+    return out

@@ -23,9 +23,9 @@ hipError_t rotquant_i8_launch(const void* x, int in_dtype, int8_t* q, float* s, 
                               hipStream_t st);
 hipError_t gemm_i8_launch(const int8_t* X, const int8_t* W, const float* xs, const float* ws,
                           const float* bias, void* out, int M, int N, int K, int epi, hipStream_t st);
-hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, const float* ws, const float* bias,
-                           const void* t, const void* U, int R, float scale, void* out, int M, int N, int K,
-                           int epi, int nsplit, void* workspace, hipStream_t st);
+hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, const float* ws, const void* bias,
+                           int bias_dt, const void* t, const void* U, int R, float scale, void* out, int M, int N,
+                           int K, int epi, int nsplit, void* workspace, hipStream_t st);
 int gemm_bf6_choose_nsplit(int M, int N, int K);
 size_t gemm_bf6_splitk_workspace(int M, int N, int nsplit);
 }  // namespace convrot
@@ -120,7 +120,7 @@ API int cr_int4_convrot_gemm_bf6(const void* A6, const void* W6, const void* xsc
     if (!bf6_k_ok(K) || M < 0 || N < 0 || epilogue < 0 || epilogue > 3) return -1;
     return (int)convrot::gemm_bf6_launch(A6, W6, reinterpret_cast<const float*>(xscale),
                                          reinterpret_cast<const float*>(wscale),
-                                         reinterpret_cast<const float*>(bias), nullptr, nullptr, 0, 0.0f, out,
+                                         bias, 0, nullptr, nullptr, 0, 0.0f, out,
                                          M, N, K, epilogue, 1, nullptr, reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -131,7 +131,7 @@ API int cr_int4_convrot_gemm_bf6_lora(const void* A6, const void* W6, const void
     if (!lora_rank_ok(R) || t == nullptr || U == nullptr) return -1;
     return (int)convrot::gemm_bf6_launch(A6, W6, reinterpret_cast<const float*>(xscale),
                                          reinterpret_cast<const float*>(wscale),
-                                         reinterpret_cast<const float*>(bias), t, U, R, scale, out, M, N, K,
+                                         bias, 0, t, U, R, scale, out, M, N, K,
                                          epilogue, 1, nullptr, reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -157,7 +157,7 @@ API int cr_int4_convrot_gemm_bf6_splitk(const void* A6, const void* W6, const vo
         return -1;
     return (int)convrot::gemm_bf6_launch(A6, W6, reinterpret_cast<const float*>(xscale),
                                          reinterpret_cast<const float*>(wscale),
-                                         reinterpret_cast<const float*>(bias), t, U, R, scale, out, M, N, K,
+                                         bias, 0, t, U, R, scale, out, M, N, K,
                                          epilogue, nsplit, workspace, reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -185,6 +185,57 @@ API int ck_int8_convrot_gemm(const void* X, const void* W, const void* xscale, c
     return cr_int8_convrot_gemm_ex(X, W, xscale, wscale, bias, out, M, N, K, out_dtype, stream);
 }
 
+// ---------------------------------------------------------------------------
+// The whole bf6 linear in one call: rotate + quantize x into B6T, the LoRA down
+// projection (R > 0), the GEMM (k-split when the library chooses it) with the
+// epilogue and the LoRA term.  Intermediates live in the caller's workspace.
+// ---------------------------------------------------------------------------
+namespace {
+struct LinPlan { size_t a6, xs, t, part, total; int nsplit; };
+size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+LinPlan lin_plan(int M, int N, int K, int R) {
+    LinPlan p{};
+    const size_t rows = (size_t)((M + 255) / 256) * 256;
+    p.nsplit = convrot::gemm_bf6_choose_nsplit(M, N, K);
+    p.a6 = 0;
+    p.xs = al256(rows * (size_t)K / 4 * 3);
+    p.t = p.xs + al256((size_t)M * 4);
+    p.part = p.t + al256((size_t)M * R * 2);
+    p.total = p.part + convrot::gemm_bf6_splitk_workspace(M, N, p.nsplit);
+    return p;
+}
+}  // namespace
+
+API size_t cr_convrot_w4a4_linear_bf6_workspace(int M, int N, int K, int R) {
+    if (M <= 0 || N <= 0 || !bf6_k_ok(K) || R < 0) return 0;
+    return lin_plan(M, N, K, R).total;
+}
+
+API int cr_convrot_w4a4_linear_bf6(const void* x, int in_dtype, const void* W6, const void* wscale, const void* bias,
+                                   int bias_dtype, const void* D, const void* U, int R, float scale, void* out,
+                                   int epilogue, int M, int N, int K, int G, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+    if (!quant_args_ok(in_dtype, M, K, G) || !bf6_k_ok(K) || K > convrot::rotquant_b6_max_k() || N < 0) return -1;
+    if (bias_dtype < 0 || bias_dtype > 2) return -1;
+    if (epilogue < 0 || epilogue > 2) return -1;
+    if (R != 0 && (!lora_rank_ok(R) || D == nullptr || U == nullptr || in_dtype == 0)) return -1;
+    if (M == 0 || N == 0) return 0;
+    const LinPlan p = lin_plan(M, N, K, R);
+    if (workspace == nullptr || workspace_bytes < p.total) return -1;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+    float* xs = reinterpret_cast<float*>(ws + p.xs);
+    hipError_t e = convrot::rotquant_b6_launch(x, in_dtype, ws + p.a6, xs, M, K, G, st);
+    if (e != hipSuccess) return (int)e;
+    if (R != 0) {
+        e = convrot::lora_down_launch(x, in_dtype, D, ws + p.t, M, K, R, st);
+        if (e != hipSuccess) return (int)e;
+    }
+    return (int)convrot::gemm_bf6_launch(ws + p.a6, W6, xs, reinterpret_cast<const float*>(wscale), bias, bias_dtype,
+                                         R ? ws + p.t : nullptr, U, R, scale, out, M, N, K, epilogue, p.nsplit,
+                                         ws + p.part, st);
+}
+
 API int cr_max_quant_k(void) { return convrot::rotquant_max_k(); }
 
-API int cr_abi_version(void) { return 4; }
+API int cr_abi_version(void) { return 5; }

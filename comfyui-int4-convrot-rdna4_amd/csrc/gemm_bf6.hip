@@ -124,7 +124,7 @@ __device__ __forceinline__ v8i bf6_operand_odd(uint4 q, uint4 p) {
 template <int EPI, int LR, bool SPLIT>
 __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
         const uint8_t* __restrict__ A6, const uint8_t* __restrict__ W6,
-        const float* __restrict__ xs, const float* __restrict__ ws, const float* __restrict__ bias,
+        const float* __restrict__ xs, const float* __restrict__ ws, const void* __restrict__ bias, int bias_dt,
         void* __restrict__ out, int M, int N, int K, LoraArgs lora, int gm, int nsplit,
         float* __restrict__ part) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds6[];
@@ -152,7 +152,7 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
 
     float* sc = reinterpret_cast<float*>(lds6 + B6_RING_BYTES);
     if constexpr (!SPLIT)
-        stage_scales(sc, xs, ws, bias, M, N, m0, n0, tid, B6_THREADS);   // visible after the loop's first barrier
+        stage_scales(sc, xs, ws, bias, bias_dt, M, N, m0, n0, tid, B6_THREADS);   // visible after the loop's first barrier
 
     // waves 0..3 copy the A chunk of a block, waves 4..7 the B chunk (6 KB each)
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -285,7 +285,7 @@ constexpr int B6R_SCR = 32 * (2 * 32 * 4 + 16);        // one 32-row f32 pass of
 template <int EPI, int LR>
 __global__ __launch_bounds__(64 * B6R_WAVES) void w4a4_bf6_splitk_reduce_kernel(
         const float* __restrict__ part, int nsplit, const float* __restrict__ xs, const float* __restrict__ ws,
-        const float* __restrict__ bias, void* __restrict__ out, int M, int N, LoraArgs lora) {
+        const void* __restrict__ bias, int bias_dt, void* __restrict__ out, int M, int N, LoraArgs lora) {
     __shared__ __attribute__((aligned(16))) float sc[EPI_SCALE_FLOATS];
     __shared__ __attribute__((aligned(16))) uint8_t scr[B6R_WAVES][B6R_SCR];
     const int lane = threadIdx.x & 63;
@@ -296,7 +296,7 @@ __global__ __launch_bounds__(64 * B6R_WAVES) void w4a4_bf6_splitk_reduce_kernel(
     const int tm = tile % tiles_m, tn = tile / tiles_m;
     const int m0 = tm * B6_BM, n0 = tn * B6_BN;
     const int wm = w >> 2, wn = w & 3;
-    stage_scales(sc, xs, ws, bias, M, N, m0, n0, threadIdx.x, 64 * B6R_WAVES);
+    stage_scales(sc, xs, ws, bias, bias_dt, M, N, m0, n0, threadIdx.x, 64 * B6R_WAVES);
     v16f acc[1][2];
     acc[0][0] = (v16f){0};
     acc[0][1] = (v16f){0};
@@ -320,7 +320,7 @@ __global__ __launch_bounds__(64 * B6R_WAVES) void w4a4_bf6_splitk_reduce_kernel(
 
 template <int EPI, int LR>
 static hipError_t launch_bf6(const uint8_t* A6, const uint8_t* W6, const float* xs, const float* ws,
-                             const float* bias, void* out, int M, int N, int K, const LoraArgs& la,
+                             const void* bias, int bias_dt, void* out, int M, int N, int K, const LoraArgs& la,
                              int nsplit, float* part, hipStream_t st) {
     constexpr int kMaxDev = 64;
     static bool attr_set[kMaxDev] = {};
@@ -339,7 +339,7 @@ static hipError_t launch_bf6(const uint8_t* A6, const uint8_t* W6, const float* 
             attr_set[dev] = true;
         }
         hipLaunchKernelGGL((w4a4_gemm_bf6_kernel<EPI, LR, false>), dim3(ntiles), dim3(B6_THREADS), B6_LDS_BYTES,
-                           st, A6, W6, xs, ws, bias, out, M, N, K, la, tile_group_rows(tiles_m), 1, nullptr);
+                           st, A6, W6, xs, ws, bias, bias_dt, out, M, N, K, la, tile_group_rows(tiles_m), 1, nullptr);
         return hipGetLastError();
     }
     // the partial kernel is the same for every epilogue and LoRA rank
@@ -351,11 +351,11 @@ static hipError_t launch_bf6(const uint8_t* A6, const uint8_t* W6, const float* 
     }
     const LoraArgs none{nullptr, nullptr, 0, 0.0f};
     hipLaunchKernelGGL((w4a4_gemm_bf6_kernel<EPI_ACC, 0, true>), dim3(ntiles * nsplit), dim3(B6_THREADS),
-                       B6_LDS_BYTES, st, A6, W6, nullptr, nullptr, nullptr, nullptr, M, N, K, none, 1, nsplit, part);
+                       B6_LDS_BYTES, st, A6, W6, nullptr, nullptr, nullptr, 0, nullptr, M, N, K, none, 1, nsplit, part);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((w4a4_bf6_splitk_reduce_kernel<EPI, LR>), dim3(ntiles * 8), dim3(64 * B6R_WAVES), 0, st,
-                       part, nsplit, xs, ws, bias, out, M, N, la);
+                       part, nsplit, xs, ws, bias, bias_dt, out, M, N, la);
     return hipGetLastError();
 }
 
@@ -367,9 +367,9 @@ hipError_t int4_to_bf6_launch(const void* src, void* dst, int rows, int K, hipSt
     return hipGetLastError();
 }
 
-hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, const float* ws, const float* bias,
-                           const void* t, const void* U, int R, float scale, void* out, int M, int N, int K,
-                           int epi, int nsplit, void* workspace, hipStream_t st) {
+hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, const float* ws, const void* bias,
+                           int bias_dt, const void* t, const void* U, int R, float scale, void* out, int M, int N,
+                           int K, int epi, int nsplit, void* workspace, hipStream_t st) {
     float* part = reinterpret_cast<float*>(workspace);
     if (M == 0 || N == 0) return hipSuccess;
     const uint8_t* a = reinterpret_cast<const uint8_t*>(A6);
@@ -377,10 +377,10 @@ hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, cons
     if (t == nullptr) {
         const LoraArgs none{nullptr, nullptr, 0, 0.0f};
         switch (epi) {
-            case EPI_F32: return launch_bf6<EPI_F32, 0>(a, w, xs, ws, bias, out, M, N, K, none, nsplit, part, st);
-            case EPI_BF16: return launch_bf6<EPI_BF16, 0>(a, w, xs, ws, bias, out, M, N, K, none, nsplit, part, st);
-            case EPI_BF16_EAGER: return launch_bf6<EPI_BF16_EAGER, 0>(a, w, xs, ws, bias, out, M, N, K, none, nsplit, part, st);
-            case EPI_ACC: return launch_bf6<EPI_ACC, 0>(a, w, xs, ws, bias, out, M, N, K, none, nsplit, part, st);
+            case EPI_F32: return launch_bf6<EPI_F32, 0>(a, w, xs, ws, bias, bias_dt, out, M, N, K, none, nsplit, part, st);
+            case EPI_BF16: return launch_bf6<EPI_BF16, 0>(a, w, xs, ws, bias, bias_dt, out, M, N, K, none, nsplit, part, st);
+            case EPI_BF16_EAGER: return launch_bf6<EPI_BF16_EAGER, 0>(a, w, xs, ws, bias, bias_dt, out, M, N, K, none, nsplit, part, st);
+            case EPI_ACC: return launch_bf6<EPI_ACC, 0>(a, w, xs, ws, bias, bias_dt, out, M, N, K, none, nsplit, part, st);
             default: return hipErrorInvalidValue;
         }
     }
@@ -389,9 +389,9 @@ hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, cons
 #define BF6_LORA_CASE(LRV)                                                                                      \
     case LRV:                                                                                                   \
         switch (epi) {                                                                                          \
-            case EPI_F32: return launch_bf6<EPI_F32, LRV>(a, w, xs, ws, bias, out, M, N, K, la, nsplit, part, st);            \
-            case EPI_BF16: return launch_bf6<EPI_BF16, LRV>(a, w, xs, ws, bias, out, M, N, K, la, nsplit, part, st);          \
-            case EPI_BF16_EAGER: return launch_bf6<EPI_BF16_EAGER, LRV>(a, w, xs, ws, bias, out, M, N, K, la, nsplit, part, st); \
+            case EPI_F32: return launch_bf6<EPI_F32, LRV>(a, w, xs, ws, bias, bias_dt, out, M, N, K, la, nsplit, part, st);            \
+            case EPI_BF16: return launch_bf6<EPI_BF16, LRV>(a, w, xs, ws, bias, bias_dt, out, M, N, K, la, nsplit, part, st);          \
+            case EPI_BF16_EAGER: return launch_bf6<EPI_BF16_EAGER, LRV>(a, w, xs, ws, bias, bias_dt, out, M, N, K, la, nsplit, part, st); \
             default: return hipErrorInvalidValue;                                                               \
         }
     switch (R / 32) {

@@ -43,17 +43,32 @@ template <int ASH> __device__ __forceinline__ float acc_float(float v) { return 
 // exact identity (x + -0 == x for every float, -0 included), so the epilogue
 // needs no per-element select.
 constexpr int EPI_SCALE_FLOATS = 3 * 256;
+
+// bias_dt: element type of the bias vector (DT_F32, DT_BF16 or DT_F16; the
+// Linear keeps its bias in fp16, so the fused path reads it as stored).
+__device__ __forceinline__ float load_bias(const void* __restrict__ bias, int bias_dt, int i) {
+    if (bias_dt == DT_F16) return f16bits_to_f32(reinterpret_cast<const uint16_t*>(bias)[i]);
+    if (bias_dt == DT_BF16) return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(bias)[i] << 16);
+    return reinterpret_cast<const float*>(bias)[i];
+}
+
 __device__ __forceinline__ void stage_scales(float* sc, const float* __restrict__ xs, const float* __restrict__ ws,
-                                             const float* __restrict__ bias, int M, int N, int m0, int n0,
-                                             int tid, int nthreads) {
+                                             const void* __restrict__ bias, int bias_dt, int M, int N, int m0,
+                                             int n0, int tid, int nthreads) {
     for (int i = tid; i < EPI_SCALE_FLOATS; i += nthreads) {
         const int part = i >> 8, k = i & 255;
         float v = 0.0f;
         if (part == 0) { if (xs && m0 + k < M) v = xs[m0 + k]; }
         else if (part == 1) { if (ws && n0 + k < N) v = ws[n0 + k]; }
-        else { v = (bias && n0 + k < N) ? bias[n0 + k] : -0.0f; }   // x + (-0) == x for every x, -0 included
+        else { v = (bias && n0 + k < N) ? load_bias(bias, bias_dt, n0 + k) : -0.0f; }   // x + (-0) == x, -0 included
         sc[i] = v;
     }
+}
+
+__device__ __forceinline__ void stage_scales(float* sc, const float* __restrict__ xs, const float* __restrict__ ws,
+                                             const float* __restrict__ bias, int M, int N, int m0, int n0,
+                                             int tid, int nthreads) {
+    stage_scales(sc, xs, ws, static_cast<const void*>(bias), DT_F32, M, N, m0, n0, tid, nthreads);
 }
 
 // Epilogue of a wave's FMT x FNT grid of 32x32 accumulator tiles at (row0, col0).

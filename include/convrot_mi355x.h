@@ -173,6 +173,28 @@ int cr_gemm_bf6_choose_nsplit(int M, int N, int K);
 size_t cr_gemm_bf6_splitk_workspace(int M, int N, int nsplit);
 
 /*
+ * The whole W4A4 linear of the Linear replacement's forward in one call:
+ *   out = epilogue(x_rot_quant @ W^T) [+ scale * (x @ D^T) @ U^T]
+ * = cr_convrot_quant_bf6 on x, cr_lora_down when R > 0 (x bf16/f16), then the
+ * bf6 GEMM (k-split when cr_gemm_bf6_choose_nsplit says so) with epilogue 0..2;
+ * the same kernels, so the same bits as those calls made one by one.  W6 is the
+ * weight in B6T (cr_int4_to_bf6), wscale f32 [N], bias [N] of bias_dtype (0 f32,
+ * 1 bf16, 2 f16: the Linear keeps biases in fp16) or NULL, D
+ * [R, K] / U [N, R] bf16 (R = 0: no LoRA).  The activation codes, scales, t and
+ * split partials live in `workspace` (>= cr_convrot_w4a4_linear_bf6_workspace
+ * bytes, reused by the next call on the same stream).  K % 128 == 0,
+ * K <= cr_max_quant_bf6_k().  No counterpart in the reference's ABI: it serves
+ * the per-call sequence of _int4/__init__.py:94-138 with one FFI crossing.
+ */
+int cr_convrot_w4a4_linear_bf6(const void* x, int in_dtype, const void* W6, const void* wscale, const void* bias,
+                               int bias_dtype, const void* D, const void* U, int R, float scale, void* out,
+                               int epilogue, int M, int N, int K, int G, void* workspace, size_t workspace_bytes,
+                               void* stream);
+
+/* Workspace bytes of cr_convrot_w4a4_linear_bf6 for this shape and LoRA rank. */
+size_t cr_convrot_w4a4_linear_bf6_workspace(int M, int N, int K, int R);
+
+/*
  * W8A8 tier (the reference's int8 ConvRot layers, _int4/int8_eager.py).
  *
  * Fused ConvRot rotation + rowwise int8 quantization:

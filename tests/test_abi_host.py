@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(native):
 
 def test_library_queries_without_gpu(native):
     lib = native.load_library()
-    assert lib.cr_abi_version() == 4
+    assert lib.cr_abi_version() == 5
     assert lib.cr_max_quant_k() == 32768
     assert lib.cr_max_quant_bf6_k() == 12288
 

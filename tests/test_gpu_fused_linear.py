@@ -1,0 +1,57 @@
+"""The single-call bf6 linear (cr_convrot_w4a4_linear_bf6, the Linear's forward
+path) against the same kernels called one by one: identical bits for every
+bias dtype, with and without LoRA, with and without a k split, and against
+the oracle's f32 epilogue."""
+import numpy as np
+import pytest
+import torch
+
+from inputs import bf16_bits, normal_bias, normal_weight, outlier_activations
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("M,N,K", [(4608, 3072, 3072), (512, 3072, 12288), (77, 640, 3840), (1, 256, 128)])
+@pytest.mark.parametrize("bias_dt", [torch.float16, torch.bfloat16, torch.float32, None])
+def test_single_call_equals_steps(backend, native, gpu, M, N, K, bias_dt):
+    print(f"fused linear M={M} N={N} K={K} bias={bias_dt}", flush=True)
+    G = backend.pick_groupsize(K)
+    x = outlier_activations(M, K, seed=M + 3).cuda()
+    qw, ws = backend.quantize_convrot_w4a4_weight(normal_weight(N, K, seed=N + 4).cuda(), convrot_groupsize=G)
+    w6 = backend.prepare_convrot_w4a4_weight_bf6(qw)
+    b = None if bias_dt is None else normal_bias(N, seed=5).to(bias_dt).cuda()
+    y = native.convrot_w4a4_linear_bf6(x, w6, ws, b, None, None, 1.0, native.EPI_BF16, G, N)
+    a6, xs = native.convrot_quant_bf6(x, G)
+    b32 = None if b is None else b.float()
+    y1 = native.int4_convrot_gemm_bf6(a6, w6, xs, ws, b32, native.EPI_BF16)
+    assert torch.equal(y, y1)
+    assert torch.equal(backend.convrot_w4a4_linear(x, qw, ws, bias=b, convrot_groupsize=G, qweight_bf6=w6), y)
+
+
+@pytest.mark.parametrize("M,N,K,R", [(4608, 3072, 3072, 32), (512, 3072, 12288, 64), (33, 513, 1024, 128)])
+def test_single_call_lora_equals_steps(backend, native, gpu, M, N, K, R):
+    x = outlier_activations(M, K, seed=M + 6).cuda()
+    qw, ws = backend.quantize_convrot_w4a4_weight(normal_weight(N, K, seed=N + 7).cuda())
+    w6 = backend.prepare_convrot_w4a4_weight_bf6(qw)
+    b = normal_bias(N, seed=8).cuda()                       # fp16, as the Linear keeps it
+    g = torch.Generator(device="cuda").manual_seed(R)
+    D = (torch.randn((R, K), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    U = (torch.randn((N, R), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    y = native.convrot_w4a4_linear_bf6(x, w6, ws, b, D, U, 1.0, native.EPI_BF16, 256, N)
+    t = native.lora_down(x, D)
+    a6, xs = native.convrot_quant_bf6(x, 256)
+    y1 = native.int4_convrot_gemm_bf6_lora(a6, w6, xs, ws, b.float(), t, U, 1.0, native.EPI_BF16)
+    assert torch.equal(y, y1)
+
+
+def test_single_call_vs_oracle(backend, native, oracle, gpu):
+    M, N, K = 96, 384, 3072
+    x = outlier_activations(M, K, seed=9)
+    w = normal_weight(N, K, seed=10)
+    b = normal_bias(N, seed=11)
+    qw, ws = backend.quantize_convrot_w4a4_weight(w.cuda())
+    y = backend.convrot_w4a4_linear(x.cuda(), qw, ws, bias=b.cuda())
+    eqx, exs, _ = oracle.rotquant(bf16_bits(x), oracle.BF16, 256)
+    acc = oracle.int_gemm(eqx, qw.cpu().numpy())
+    want = oracle.epilogue_f32(acc, exs, ws.cpu().numpy(), b.float().numpy(), out_bf16=True)
+    assert np.array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), want)
