@@ -55,7 +55,11 @@ constexpr int kPad = 17;         // fp64 words per lane slot in the transpose bu
 // (every value is exact: sums of inputs times powers of two; fma keeps one op)
 __device__ __forceinline__ void h4_stage(double& a, double& b, double& c, double& d, double scale) {
     const double S = (scale == 1.0) ? ((a + b) + (c + d)) : ((a + b) + (c + d)) * scale;
-    const double t = -2.0 * scale;
+    double t = -2.0 * scale;
+    // -2 is an inline constant of the 3-operand fma; any other factor would be
+    // a literal, which only the 2-operand fmac takes (plus a copy of S per
+    // output): hold it in an SGPR pair instead
+    if (scale != 1.0) asm("" : "+s"(t));
     const double na = __builtin_fma(t, d, S), nb = __builtin_fma(t, c, S);
     const double nc = __builtin_fma(t, b, S), nd = __builtin_fma(t, a, S);
     a = na; b = nb; c = nc; d = nd;

@@ -86,6 +86,8 @@ def _load():
     lib.orc_round_double_bits.restype = ctypes.c_uint16
     lib.orc_round_to.argtypes = [ctypes.c_float, i]
     lib.orc_round_to.restype = ctypes.c_float
+    lib.orc_num_threads.argtypes = []
+    lib.orc_num_threads.restype = i
     lib.orc_f32_to_bf16.argtypes = [ctypes.c_float]
     lib.orc_f32_to_bf16.restype = ctypes.c_uint16
     _lib = lib
@@ -350,3 +352,8 @@ def linear_w8a8(x, dt, qweight, wscales, bias=None, G=256, out_bf16=True):
     q, xs, _ = rotquant8(x, dt, G)
     acc = int8_gemm(q, qweight)
     return epilogue_f32(acc, xs, wscales, bias, out_bf16=out_bf16)
+
+
+def num_threads() -> int:
+    """Threads of the oracle's parallel row loops (OpenMP, OMP_NUM_THREADS)."""
+    return int(_load().orc_num_threads())

@@ -17,7 +17,7 @@ def build() -> str:
     src = os.path.join(_HERE, "convrot_oracle.c")
     out = os.path.join(_HERE, "liboracle.so")
     tmp = out + ".tmp"
-    cmd = ["gcc", "-O2", "-std=gnu11", "-fno-fast-math", "-ffp-contract=off", "-Wall",
+    cmd = ["gcc", "-O2", "-std=gnu11", "-fno-fast-math", "-ffp-contract=off", "-Wall", "-fopenmp",
            "-shared", "-fPIC", src, "-o", tmp, "-lm"]
     subprocess.run(cmd, check=True)
     os.replace(tmp, out)

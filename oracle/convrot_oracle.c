@@ -2,7 +2,8 @@
  * CPU oracle for the W4A4 ConvRot linear path.  TEST INFRASTRUCTURE ONLY:
  * nothing in the shipped package links, loads or calls this file; only
  * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it,
- * and only as the checker.
+ * and only as the checker.  Row loops run in parallel with OpenMP (rows are
+ * independent; the arithmetic of every row is unchanged).
  *
  * It restates the reference eager path (pure torch) in plain C, with every
  * rounding step made explicit.  Each function names the reference lines it
@@ -25,6 +26,9 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
 
 #define DT_F32 0
 #define DT_BF16 1
@@ -269,9 +273,12 @@ int orc_rotate(const void* x, int dt, int M, int K, int G, void* out) {
     fmt_t f = fmt_of(dt);
     int lg = log4i(G);
     int halflog = lg;                          /* sqrt(G) = 2^lg */
+#pragma omp parallel reduction(+ : nexact)
+    {
     double* v = (double*)malloc(sizeof(double) * G);
     int* mm = (int*)malloc(sizeof(int) * G);
     int* ee = (int*)malloc(sizeof(int) * G);
+#pragma omp for schedule(static)
     for (int m = 0; m < M; ++m) {
         for (int g = 0; g < K / G; ++g) {
             size_t base = (size_t)m * K + (size_t)g * G;
@@ -310,6 +317,7 @@ int orc_rotate(const void* x, int dt, int M, int K, int G, void* out) {
         }
     }
     free(v); free(mm); free(ee);
+    }
     return nexact;
 }
 
@@ -361,6 +369,7 @@ static int code_of(float t, int stochastic, float u, int dt) {
 void orc_quant_rows(const void* xr, int dt, int M, int K, const void* noise,
                     int8_t* packed, float* scales, int8_t* codes /* nullable, [M,K] */) {
     float lo = clamp_floor_value(dt);
+#pragma omp parallel for schedule(static)
     for (int m = 0; m < M; ++m) {
         size_t base = (size_t)m * K;
         float a = 0.0f;
@@ -405,6 +414,7 @@ int orc_rotquant(const void* x, int dt, int M, int K, int G, const void* noise,
 
 void orc_quant_rows8(const void* xr, int dt, int M, int K, int8_t* q8, float* scales) {
     float lo = clamp_floor_value(dt);
+#pragma omp parallel for schedule(static)
     for (int m = 0; m < M; ++m) {
         size_t base = (size_t)m * K;
         float a = 0.0f;
@@ -440,6 +450,7 @@ int orc_rotquant8(const void* x, int dt, int M, int K, int G, int8_t* q8, float*
 /* W8A8 accumulators acc[m,n] = sum_k x[m,k] * w[n,k], exact in int64 and    */
 /* returned as int32 (|acc| <= 127^2 K < 2^31 for K < 133000).              */
 void orc_int8_gemm(const int8_t* X, const int8_t* W, int M, int N, int K, int32_t* acc) {
+#pragma omp parallel for schedule(static)
     for (int m = 0; m < M; ++m) {
         const int8_t* a = X + (size_t)m * K;
         for (int n = 0; n < N; ++n) {
@@ -470,6 +481,7 @@ void orc_int_gemm(const int8_t* Xp, const int8_t* Wp, int M, int N, int K, int32
     int8_t* wc = (int8_t*)malloc((size_t)N * K);
     orc_unpack(Xp, (size_t)M * K / 2, xc);
     orc_unpack(Wp, (size_t)N * K / 2, wc);
+#pragma omp parallel for schedule(static)
     for (int m = 0; m < M; ++m) {
         const int8_t* a = xc + (size_t)m * K;
         for (int n = 0; n < N; ++n) {
@@ -496,6 +508,7 @@ void orc_int_gemm(const int8_t* Xp, const int8_t* Wp, int M, int N, int K, int32
  * out_bf16 != 0 rounds the final value once to bf16 (bits in out16). */
 void orc_epilogue_f32(const int32_t* acc, const float* xs, const float* ws, const float* bias,
                       int M, int N, int out_bf16, float* out32, uint16_t* out16) {
+#pragma omp parallel for schedule(static)
     for (int m = 0; m < M; ++m)
         for (int n = 0; n < N; ++n) {
             volatile float t = (float)acc[(size_t)m * N + n] * xs[m];
@@ -511,6 +524,7 @@ void orc_epilogue_f32(const int32_t* acc, const float* xs, const float* ws, cons
  * each product/sum formed in fp32 and rounded to bf16, as torch does. */
 void orc_epilogue_eager_bf16(const int32_t* acc, const float* xs, const float* ws, const float* bias,
                              int M, int N, uint16_t* out16) {
+#pragma omp parallel for schedule(static)
     for (int m = 0; m < M; ++m) {
         float xsb = orc_round_to(xs[m], DT_BF16);
         for (int n = 0; n < N; ++n) {
@@ -522,6 +536,15 @@ void orc_epilogue_eager_bf16(const int32_t* acc, const float* xs, const float* w
             out16[(size_t)m * N + n] = orc_f32_to_bf16(o4);
         }
     }
+}
+
+/* threads the row loops above use (OpenMP; OMP_NUM_THREADS) */
+int orc_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
 }
 
 /* scalar conversion entry points for the python side */
