@@ -91,8 +91,9 @@ __global__ __launch_bounds__(256) void int4_to_bf6t_kernel(const uint8_t* __rest
 // tile 128 x 64 = 4 x 2 MFMA tiles of 32 x 32).  A stage is the A chunk and
 // the B chunk of one 128-k block (48 KB), copied by global_load_lds_dwordx4
 // (6 contiguous 1 KB instructions per wave), three stages deep.  Per block
-// and wave: 2 k steps x 8 MFMAs, each operand one ds_read_b128 (P part) + one
-// ds_read_b64 (Q part).  The epilogue goes through LDS (epilogue_lds).
+// and wave: 2 k steps x 8 MFMAs over 9 ds_read_b128 fragment reads per k step
+// (6 P pieces, 3 Q pieces each shared by two row tiles).  The epilogue goes
+// through LDS (epilogue_lds).
 // ---------------------------------------------------------------------------
 
 constexpr int B6_BM = 256, B6_BN = 256;
@@ -105,12 +106,14 @@ constexpr int B6_LDS_BYTES = B6_RING_BYTES + EPI_SCALE_FLOATS * 4;
 constexpr int BF6_FMT = 3;                                 // f8f6f4 operand format code of BF6 (E3M2)
 constexpr int E8M0_ONE = 127;                              // block scale 2^0
 
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
 // operand of an even row tile: d0..d3 from its P piece, d4..d5 from bytes 0..7 of the Q piece
-__device__ __forceinline__ v8i bf6_operand_even(uint4 p, uint4 q) {
+__device__ __forceinline__ v8i bf6_operand_even(v4u p, v4u q) {
     return (v8i){(int)p.x, (int)p.y, (int)p.z, (int)p.w, (int)q.x, (int)q.y, 0, 0};
 }
 // operand of an odd row tile: d0..d1 from bytes 8..15 of the Q piece, d2..d5 from its P piece
-__device__ __forceinline__ v8i bf6_operand_odd(uint4 q, uint4 p) {
+__device__ __forceinline__ v8i bf6_operand_odd(v4u q, v4u p) {
     return (v8i){(int)q.z, (int)q.w, (int)p.x, (int)p.y, (int)p.z, (int)p.w, 0, 0};
 }
 
@@ -188,68 +191,88 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
             offQb[s2] = B6_CHUNK + b6_q_off(rb, g);
         }
     }
-    // the 6 fragments of k step s2 of the block in the stage at byte offset st:
-    // 6 P reads and 3 Q reads, all 16 bytes
-    auto read_step = [&](uint32_t st, int s2, v8i (&fa)[4], v8i (&fb)[2]) {
+    // Fragments of one k step: P pieces of the 4 A and 2 B row tiles, and the 16-byte
+    // Q pieces shared by row tiles (0, 1) and (2, 3) of A and (0, 1) of B.
+    // (native vector registers: a HIP uint4 assignment from LDS would be an
+    // aggregate copy through private memory)
+    struct Frags { v4u pa[4], qa[2], pb[2], qb; };
+    // read r (0..8) of k step s2 of the block in the stage at byte offset st
+    auto read_one = [&](uint32_t st, int s2, int r, Frags& f) __attribute__((always_inline)) {
         const uint8_t* base = lds6 + st;
-        uint4 pa[4], pb[2], qa[2], qb;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pa[i] = *reinterpret_cast<const uint4*>(base + offPa[s2] + i * 2048);
-#pragma unroll
-        for (int p = 0; p < 2; ++p) qa[p] = *reinterpret_cast<const uint4*>(base + offQa[s2] + p * 2048);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) pb[j] = *reinterpret_cast<const uint4*>(base + offPb[s2] + j * 2048);
-        qb = *reinterpret_cast<const uint4*>(base + offQb[s2]);
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            fa[2 * p] = bf6_operand_even(pa[2 * p], qa[p]);
-            fa[2 * p + 1] = bf6_operand_odd(qa[p], pa[2 * p + 1]);
-        }
-        fb[0] = bf6_operand_even(pb[0], qb);
-        fb[1] = bf6_operand_odd(qb, pb[1]);
+        if (r < 4) f.pa[r] = *reinterpret_cast<const v4u*>(base + offPa[s2] + r * 2048);
+        else if (r < 6) f.qa[r - 4] = *reinterpret_cast<const v4u*>(base + offQa[s2] + (r - 4) * 2048);
+        else if (r < 8) f.pb[r - 6] = *reinterpret_cast<const v4u*>(base + offPb[s2] + (r - 6) * 2048);
+        else f.qb = *reinterpret_cast<const v4u*>(base + offQb[s2]);
     };
-    auto mfma_step = [&](const v8i (&fa)[4], const v8i (&fb)[2]) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(   // transposed tile
-                        fb[j], fa[i], acc[i][j], BF6_FMT, BF6_FMT, 0, E8M0_ONE, 0, E8M0_ONE);
+    // MFMA t (0..7) of a k step: A row tile t / 2 against B row tile t % 2
+    auto mfma_one = [&](const Frags& f, int t) __attribute__((always_inline)) {
+        const int i = t >> 1, j = t & 1;
+        const v4u q = f.qa[i >> 1], p = f.pa[i], qb = f.qb, pb = f.pb[j];
+        const v8i fa = (i & 1) ? bf6_operand_odd(q, p) : bf6_operand_even(p, q);
+        const v8i fb = j ? bf6_operand_odd(qb, pb) : bf6_operand_even(pb, qb);
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(   // transposed tile
+                fb, fa, acc[i][j], BF6_FMT, BF6_FMT, 0, E8M0_ONE, 0, E8M0_ONE);
     };
-    auto issue_clamped = [&](int kb) {     // past the end: re-copy the last block into a free stage
+    // the reads issued after MFMA slot t, in the order the next k step's MFMAs
+    // consume them: pb0 qb | pa0 qa0 | pb1 pa1 | pa2 qa1 | pa3 (all in the first
+    // five slots, so they have landed when the phase ends)
+    auto reads_after = [&](int t, uint32_t st, int s2, Frags& f) __attribute__((always_inline)) {
+        if (t == 0) { read_one(st, s2, 6, f); read_one(st, s2, 8, f); }
+        if (t == 1) { read_one(st, s2, 0, f); read_one(st, s2, 4, f); }
+        if (t == 2) { read_one(st, s2, 7, f); read_one(st, s2, 1, f); }
+        if (t == 3) { read_one(st, s2, 2, f); read_one(st, s2, 5, f); }
+        if (t == 4) read_one(st, s2, 3, f);
+    };
+    // DMA instruction j of block kb (past the end: a repeat of the last block)
+    auto dma_one = [&](int kb, int j) __attribute__((always_inline)) {
         const uint32_t st = my_lds + (kb % B6_STAGES) * B6_STAGE_BYTES;
-        const uint8_t* src = my_src + (size_t)min(kb, nkb - 1) * B6_CHUNK;
-#pragma unroll
-        for (int j = 0; j < B6_LOADS; ++j) dma16(st + j * 1024, src + j * 1024);
+        dma16(st + j * 1024, my_src + (size_t)min(kb, nkb - 1) * B6_CHUNK + j * 1024);
     };
 
-    // Software pipeline across the block barrier.  Per block kb: read the
-    // fragments of k step 1, run the MFMAs of k step 0 (their fragments were read
-    // one phase earlier), wait for block kb+1 and pass the barrier (every wave has
-    // then finished reading block kb, whose stage takes block kb+3), read the
-    // first fragments of block kb+1, run the MFMAs of k step 1.  Each phase's LDS
-    // latency is covered by the other phase's MFMAs, and the loop body is one
-    // branch-free block (sched_barrier(0) pins the phase order; past the end the
-    // copies and reads are harmless repeats).
-    v8i fa0[4], fb0[2], fa1[4], fb1[2];
-    issue_clamped(0);
-    issue_clamped(1);
+    // Hand-scheduled pipeline, two phases per 128-k block kb, three stages, copies
+    // issued three blocks ahead.  Phase A: the 8 MFMAs of k step 0 (fragments read
+    // in the previous phase B), the first five followed by the fragment reads of
+    // k step 1.  Then wait until this wave's copy of block kb+1 has landed and its
+    // reads of block kb are done, and pass the barrier: the copies of block kb+1
+    // are visible and no wave reads block kb's stage any more.  Phase B: the 8
+    // MFMAs of k step 1, the first six followed by one DMA instruction of block
+    // kb+3 (into block kb's stage) and the fragment reads of k step 0 of block
+    // kb+1.  Interleaving keeps the matrix pipe fed while the reads and copies
+    // issue; sched_barrier(0) pins every slot.
+    Frags F0, F1;
+#pragma unroll
+    for (int j = 0; j < B6_LOADS; ++j) dma_one(0, j);
+#pragma unroll
+    for (int j = 0; j < B6_LOADS; ++j) dma_one(1, j);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(B6_LOADS));          // block 0 landed, block 1 in flight
     __syncthreads();
-    issue_clamped(2);
-    read_step(0, 0, fa0, fb0);
+#pragma unroll
+    for (int j = 0; j < B6_LOADS; ++j) dma_one(2, j);
+#pragma unroll
+    for (int r = 0; r < 9; ++r) read_one(0, 0, r, F0);
     uint32_t st_cur = 0;                                      // stage of block kb
     for (int kb = 0; kb < nkb; ++kb) {
         const uint32_t st_nxt = st_cur == (B6_STAGES - 1) * B6_STAGE_BYTES ? 0u : st_cur + B6_STAGE_BYTES;
-        read_step(st_cur, 1, fa1, fb1);
-        mfma_step(fa0, fb0);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            mfma_one(F0, t);
+            __builtin_amdgcn_sched_barrier(0);
+            reads_after(t, st_cur, 1, F1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // this wave's copy of block kb+1 landed (block kb+2 in flight) and its
+        // reads of block kb done: after the barrier block kb's stage is free
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(B6_LOADS) & 0xc07f);
+        __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(B6_LOADS));      // block kb+1 landed, block kb+2 in flight
-        __syncthreads();
-        issue_clamped(kb + 3);
-        read_step(st_nxt, 0, fa0, fb0);
-        __builtin_amdgcn_sched_barrier(0);
-        mfma_step(fa1, fb1);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            mfma_one(F1, t);
+            __builtin_amdgcn_sched_barrier(0);
+            if (t < B6_LOADS) dma_one(kb + 3, t);
+            reads_after(t, st_nxt, 0, F0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         st_cur = st_nxt;
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));                 // the copies past the end have landed
