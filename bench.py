@@ -169,22 +169,34 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    # timed region: K steps, bracketed by synchronize on both sides
-    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
-           for _ in calls] for _ in range(args.steps)]
+    # timed region: K steps, bracketed by synchronize on both sides, with no
+    # event between the launches (an event record is a packet of its own on the
+    # stream and would be timed as part of the step)
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     t_start.record(stream)
     for s in range(args.steps):
-        step(ev[s])
+        step()
     t_end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = t_start.elapsed_time(t_end) / args.steps
 
-    # per-launch durations (HIP events on the launch stream)
+    # per-launch durations: the same K steps again, each launch bracketed by HIP
+    # events on the launch stream
+    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
+           for _ in calls] for _ in range(args.steps)]
+    e_start = torch.cuda.Event(enable_timing=True)
+    e_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e_start.record(stream)
+    for s in range(args.steps):
+        step(ev[s])
+    e_end.record(stream)
+    torch.cuda.synchronize()
+    ms_step_events = e_start.elapsed_time(e_end) / args.steps
     dur = {}
     for s in range(args.steps):
         for j, (kind, i, _, _) in enumerate(calls):
@@ -270,6 +282,7 @@ def main():
         "detail": detail,
         "cpu_baseline": cpu,
         "host_wall_s": round(wall, 3),
+        "ms_per_step_with_kernel_events": round(ms_step_events, 4),
     }
     if copy_cal:
         line["copy_calibration"] = copy_cal
