@@ -285,6 +285,10 @@ __global__ __launch_bounds__(kMaxThreads) void rotquant_kernel(
 
 constexpr int kWaves = 4;      // independent waves per workgroup
 
+typedef unsigned v16u __attribute__((ext_vector_type(16)));
+typedef unsigned v6u __attribute__((ext_vector_type(6)));
+typedef __bf16 v32bf __attribute__((ext_vector_type(32)));
+
 template <int DT>
 struct ChunkRegs { uint4 r[DT == DT_F32 ? 4 : 2]; };
 
@@ -387,6 +391,22 @@ __device__ __forceinline__ void b6_store_half(int8_t* out, int row, int K, int k
     }
 }
 
+// Store the 32 codes of group k0 .. k0+31 of `row` (6 packed dwords, k0 % 32 ==
+// 0) at their place in a B6T buffer (placement: b6t_layout.h).
+__device__ __forceinline__ void b6_store_group(int8_t* out, int row, int K, int k0, const uint32_t (&d)[6]) {
+    const int kb = k0 >> 7, g = (k0 >> 5) & 3, r = row & 255;
+    uint8_t* chunk = reinterpret_cast<uint8_t*>(out) + ((size_t)(row >> 8) * (K >> 7) + kb) * B6_CHUNK;
+    uint32_t* p = reinterpret_cast<uint32_t*>(chunk + b6_p_off(r, g));
+    uint32_t* q = reinterpret_cast<uint32_t*>(chunk + b6_q_off(r, g));
+    if (!b6_odd_tile(r)) {          // P = d0..d3, Q bytes 0..7 = d4..d5
+        *reinterpret_cast<uint4*>(p) = make_uint4(d[0], d[1], d[2], d[3]);
+        *reinterpret_cast<uint2*>(q) = make_uint2(d[4], d[5]);
+    } else {                        // P = d2..d5, Q bytes 8..15 = d0..d1
+        *reinterpret_cast<uint4*>(p) = make_uint4(d[2], d[3], d[4], d[5]);
+        *reinterpret_cast<uint2*>(q + 2) = make_uint2(d[0], d[1]);
+    }
+}
+
 // OUT selects the code format: OUT_PACK4 packed nibbles; OUT_B6T the B6T
 // layout of the bf6 GEMM (b6t_layout.h; K % 128 == 0; rows M .. ceil(M/256)*256
 // get zero codes); OUT_I8 the int8 tier's plain int8 codes (scale a / 127,
@@ -397,20 +417,27 @@ template <int DT, int G, int NPMAX, int OUT>
 __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
         const void* __restrict__ x, int8_t* __restrict__ qout, float* __restrict__ sout, int M, int K) {
     constexpr int LPG = G / kChunk;
+    constexpr bool B6 = OUT == OUT_B6T;
+    // code reorder buffer per wave: bytes (64 chunks x 16) for the integer
+    // outputs; for B6T the rounded codes as bf16, chunk ch at (ch / 16) * 544 +
+    // (ch % 16) * 32 bytes (the pad spreads the four 16-lane groups over the banks)
+    constexpr int kB6Group = 544;
     __shared__ double tbuf_all[kWaves][64 * kPad];
-    __shared__ uint32_t cbuf_all[kWaves][64 * 4];
+    __shared__ __attribute__((aligned(16))) uint32_t cbuf_all[kWaves][B6 ? kB6Group : 64 * 4];
 
     const int lane = threadIdx.x & 63;
-    const int wv = threadIdx.x >> 6;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: rows are per wave
     double* tbuf = tbuf_all[wv];
     uint8_t* cb = reinterpret_cast<uint8_t*>(cbuf_all[wv]);
+    auto b6_slot = [&](int ch, int pos) {
+        return reinterpret_cast<uint16_t*>(cb + (ch >> 4) * kB6Group + (ch & 15) * 32) + pos;
+    };
     const int nwaves = gridDim.x * kWaves;
     const int nchunks = K / kChunk;
     const int np = (nchunks + 63) >> 6;
     const int gl = lane % LPG;
     const int gfirst = lane - gl;
     const float kMagic = 12582912.0f;
-    constexpr bool B6 = OUT == OUT_B6T;
     constexpr float QMAX = OUT == OUT_I8 ? 127.0f : 7.0f;
 
     ChunkRegs<DT> nxt;
@@ -518,23 +545,44 @@ __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
                         z0 = zz[0];
                         z1 = zz[1];
                     }
-                    // low byte of the float bits of z + 1.5*2^23 is rint_even(z) (two's complement)
                     const int e0 = final_elem<G>(gl, i), e1 = final_elem<G>(gl, i + 1);
-                    cb[(gfirst + e0 / kChunk) * 16 + (e0 % kChunk)] = (uint8_t)__float_as_uint(z0 + kMagic);
-                    cb[(gfirst + e1 / kChunk) * 16 + (e1 % kChunk)] = (uint8_t)__float_as_uint(z1 + kMagic);
+                    if constexpr (B6) {
+                        // rint_even(z) as a float (+0 for zero), kept as its bf16 bits (exact:
+                        // an integer of magnitude <= 7)
+                        const float q0 = (z0 + kMagic) - kMagic, q1 = (z1 + kMagic) - kMagic;
+                        *b6_slot(gfirst + e0 / kChunk, e0 % kChunk) = (uint16_t)(__float_as_uint(q0) >> 16);
+                        *b6_slot(gfirst + e1 / kChunk, e1 % kChunk) = (uint16_t)(__float_as_uint(q1) >> 16);
+                    } else {
+                        // low byte of the float bits of z + 1.5*2^23 is rint_even(z) (two's complement)
+                        cb[(gfirst + e0 / kChunk) * 16 + (e0 % kChunk)] = (uint8_t)__float_as_uint(z0 + kMagic);
+                        cb[(gfirst + e1 / kChunk) * 16 + (e1 % kChunk)] = (uint8_t)__float_as_uint(z1 + kMagic);
+                    }
                 }
                 wave_sync();
-                const uint4 w = reinterpret_cast<const uint4*>(cb)[lane];
+                uint4 w = {}, gq[4];        // gq: filled and used on even lanes only (B6T)
+                if constexpr (B6) {
+                    // the even lane of a pair reads the pair's 32 codes (64 bytes)
+                    if ((lane & 1) == 0) {
+#pragma unroll
+                        for (int h = 0; h < 4; ++h) gq[h] = reinterpret_cast<const uint4*>(b6_slot(lane, 0))[h];
+                    }
+                } else {
+                    w = reinterpret_cast<const uint4*>(cb)[lane];
+                }
                 wave_sync();
                 if (OUT == OUT_I8 && ok) {
                     *reinterpret_cast<uint4*>(qout + (size_t)row * K + (size_t)c * kChunk) = w;
                 } else if (B6 && ok) {
-                    // lane pair (2g', 2g'+1) holds the 32 codes of one MFMA group: the even
-                    // lane its dwords 0..2, the odd lane dwords 3..5
-                    const uint32_t c4[4] = {bf6_bytes(w.x), bf6_bytes(w.y), bf6_bytes(w.z), bf6_bytes(w.w)};
-                    uint32_t d[3];
-                    bf6_pack16(c4, d);
-                    b6_store_half(qout, row, K, c * kChunk, d);
+                    // chunks (2g', 2g'+1) are the 32 codes of one MFMA group: the even lane
+                    // converts them (bf16 values, element order) with the 32-wide BF6
+                    // converter and stores the group's 6 dwords
+                    if ((lane & 1) == 0) {
+                        const v16u words = {gq[0].x, gq[0].y, gq[0].z, gq[0].w, gq[1].x, gq[1].y, gq[1].z, gq[1].w,
+                                            gq[2].x, gq[2].y, gq[2].z, gq[2].w, gq[3].x, gq[3].y, gq[3].z, gq[3].w};
+                        const v6u r = __builtin_amdgcn_cvt_scalef32_pk32_bf6_bf16(__builtin_bit_cast(v32bf, words), 1.0f);
+                        const uint32_t d[6] = {r[0], r[1], r[2], r[3], r[4], r[5]};
+                        b6_store_group(qout, row, K, c * kChunk, d);
+                    }
                 } else if (ok) {
                     const uint32_t ws[4] = {w.x & 0x0f0f0f0fu, w.y & 0x0f0f0f0fu, w.z & 0x0f0f0f0fu,
                                             w.w & 0x0f0f0f0fu};
