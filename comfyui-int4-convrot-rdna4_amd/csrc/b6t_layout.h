@@ -61,40 +61,4 @@ constexpr uint32_t bf6_code_of_int(int q) {
 }
 static_assert(bf6_code_of_int(7) == 23 && bf6_code_of_int(-8) == 56 && bf6_code_of_int(3) == 18, "bf6");
 
-// codes of the int4 values whose two's complement nibbles are base .. base+3,
-// one per byte (the byte lookup table of bf6_bytes)
-constexpr uint32_t bf6_lut4(int base) {
-    uint32_t t = 0;
-    for (int i = 0; i < 4; ++i) {
-        const int n = base + i;
-        t |= bf6_code_of_int(n >= 8 ? n - 16 : n) << (8 * i);
-    }
-    return t;
-}
-
-// Four bytes whose low nibbles are int4 codes (two's complement) -> their
-// four BF6 codes, one per byte: two v_perm_b32 byte lookups (nibbles 0..7 and
-// 8..15; selector values 0..3 take bytes of the second source, 4..7 of the
-// first) and a per-byte select on nibble bit 3.
-__device__ __forceinline__ uint32_t bf6_bytes(uint32_t w) {
-    const uint32_t sel = w & 0x07070707u;
-    const uint32_t lo = __builtin_amdgcn_perm(bf6_lut4(4), bf6_lut4(0), sel);
-    const uint32_t hi = __builtin_amdgcn_perm(bf6_lut4(12), bf6_lut4(8), sel);
-    const uint32_t neg = ((w >> 3) & 0x01010101u) * 0xFFu;       // 0xFF in bytes with nibble bit 3
-    return (hi & neg) | (lo & ~neg);
-}
-
-// 16 BF6 codes (one per byte, 4 per dword) -> 96 packed bits (code e at 6e)
-__device__ __forceinline__ void bf6_pack16(const uint32_t (&c)[4], uint32_t (&d)[3]) {
-    uint32_t f[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const uint32_t w = c[k];
-        f[k] = (w & 0x3Fu) | ((w >> 2) & 0xFC0u) | ((w >> 4) & 0x3F000u) | ((w >> 6) & 0xFC0000u);
-    }
-    d[0] = f[0] | (f[1] << 24);
-    d[1] = (f[1] >> 8) | (f[2] << 16);
-    d[2] = (f[2] >> 16) | (f[3] << 8);
-}
-
 }  // namespace convrot

@@ -365,32 +365,6 @@ __device__ __forceinline__ float jam_to_f32(double d) {
 }
 
 
-// Store the 16 codes of elements k0 .. k0+15 of `row` (3 packed dwords, k0 % 16
-// == 0) at their place in a B6T buffer: the first half of an MFMA group holds
-// its dwords d0..d2, the second half d3..d5 (placement: b6t_layout.h).
-__device__ __forceinline__ void b6_store_half(int8_t* out, int row, int K, int k0, const uint32_t (&d)[3]) {
-    const int kb = k0 >> 7, g = (k0 >> 5) & 3, r = row & 255;
-    uint8_t* chunk = reinterpret_cast<uint8_t*>(out) + ((size_t)(row >> 8) * (K >> 7) + kb) * B6_CHUNK;
-    uint32_t* p = reinterpret_cast<uint32_t*>(chunk + b6_p_off(r, g));
-    uint32_t* q = reinterpret_cast<uint32_t*>(chunk + b6_q_off(r, g));
-    const bool second = ((k0 >> 4) & 1) != 0;
-    if (!b6_odd_tile(r)) {          // P = d0..d3, Q bytes 0..7 = d4..d5
-        if (!second) {
-            p[0] = d[0]; p[1] = d[1]; p[2] = d[2];
-        } else {
-            p[3] = d[0];
-            *reinterpret_cast<uint2*>(q) = make_uint2(d[1], d[2]);
-        }
-    } else {                        // P = d2..d5, Q bytes 8..15 = d0..d1
-        if (!second) {
-            *reinterpret_cast<uint2*>(q + 2) = make_uint2(d[0], d[1]);
-            p[0] = d[2];
-        } else {
-            p[1] = d[0]; p[2] = d[1]; p[3] = d[2];
-        }
-    }
-}
-
 // Store the 32 codes of group k0 .. k0+31 of `row` (6 packed dwords, k0 % 32 ==
 // 0) at their place in a B6T buffer (placement: b6t_layout.h).
 __device__ __forceinline__ void b6_store_group(int8_t* out, int row, int K, int k0, const uint32_t (&d)[6]) {
@@ -601,9 +575,9 @@ __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
     }
     if constexpr (B6) {   // zero codes in the padding rows of the last 256-row tile
         const int mpad = (M + 255) & ~255;
-        const uint32_t z[3] = {0u, 0u, 0u};
+        const uint32_t z[6] = {0u, 0u, 0u, 0u, 0u, 0u};
         for (int prow = M + blockIdx.x * kWaves + wv; prow < mpad; prow += nwaves)
-            for (int c = lane; c < nchunks; c += 64) b6_store_half(qout, prow, K, c * kChunk, z);
+            for (int k0 = 32 * lane; k0 < K; k0 += 32 * 64) b6_store_group(qout, prow, K, k0, z);
     }
 }
 
