@@ -355,12 +355,17 @@ __device__ __forceinline__ float held(const Held<DT>& h, int i) {
 // (see round_f64_to_dt): rounding the result once to bf16/f16 equals rounding
 // the fp64 value once.  Monotone, so the max of jammed values rounds to the
 // max of the rounded values.
-// The sticky bit goes to fp64 mantissa bit 29, the last bit a float keeps,
-// so the conversion is exact; mantissa bits 31..29 of the input are below the
-// bf16 / f16 guard bit and only their "any set" matters.
+// The whole low dword is below the bf16 / f16 guard bit, so only whether it
+// is nonzero matters.  It is replaced by the float bits of its value as an
+// unsigned integer: 0 for 0, else a pattern in [0x3F800000, 0x4F800000] whose
+// bits 31..29 (the last three a float keeps) are not all clear and stay so
+// after the rounding to float, which cannot carry past bit 31.  Below those
+// bits the replacement is less than one unit of bit 32, so it changes no
+// rounding decision of the conversion either (subnormal results included).
+// One conversion instead of a compare and a select.
 __device__ __forceinline__ float jam_to_f32(double d) {
     const uint64_t u = (uint64_t)__double_as_longlong(d);
-    const uint32_t lo = min((uint32_t)u, 1u) << 29;
+    const uint32_t lo = __float_as_uint((float)(uint32_t)u);
     return (float)__longlong_as_double((long long)((u & 0xffffffff00000000ull) | lo));
 }
 
