@@ -397,17 +397,20 @@ __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
         const void* __restrict__ x, int8_t* __restrict__ qout, float* __restrict__ sout, int M, int K) {
     constexpr int LPG = G / kChunk;
     constexpr bool B6 = OUT == OUT_B6T;
-    // code reorder buffer per wave: bytes (64 chunks x 16) for the integer
-    // outputs; for B6T the rounded codes as bf16, chunk ch at (ch / 16) * 544 +
-    // (ch % 16) * 32 bytes (the pad spreads the four 16-lane groups over the banks)
+    // Per-wave LDS: the fp64 transpose buffer of the rotation passes, reused as
+    // the code reorder buffer of the quantize loop (which runs after every pass
+    // of the row; a wave's LDS operations complete in order).  Codes: bytes (64
+    // chunks x 16) for the integer outputs; for B6T the rounded codes as bf16,
+    // chunk ch at (ch / 16) * 544 + (ch % 16) * 32 bytes (the pad spreads the
+    // four 16-lane groups over the banks).  One buffer keeps 4 workgroups per CU.
     constexpr int kB6Group = 544;
-    __shared__ double tbuf_all[kWaves][64 * kPad];
-    __shared__ __attribute__((aligned(16))) uint32_t cbuf_all[kWaves][B6 ? kB6Group : 64 * 4];
+    __shared__ __attribute__((aligned(16))) double tbuf_all[kWaves][64 * kPad];
+    static_assert(64 * kPad * 8 >= (B6 ? 4 * kB6Group : 64 * 16), "code buffer");
 
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: rows are per wave
     double* tbuf = tbuf_all[wv];
-    uint8_t* cb = reinterpret_cast<uint8_t*>(cbuf_all[wv]);
+    uint8_t* cb = reinterpret_cast<uint8_t*>(tbuf_all[wv]);
     auto b6_slot = [&](int ch, int pos) {
         return reinterpret_cast<uint16_t*>(cb + (ch >> 4) * kB6Group + (ch & 15) * 32) + pos;
     };
