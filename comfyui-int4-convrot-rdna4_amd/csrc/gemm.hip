@@ -243,6 +243,79 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
     const int frow = lane & 31;
     const int fhalf = lane >> 5;
 
+    if constexpr (I8) {
+        // W8A8: hand-scheduled loop, two phases per 64-k block kb (k steps of 32).
+        // Phase A: the 8 MFMAs of k step 0 (fragments read in the previous phase
+        // B), the first five followed by the fragment reads of k step 1.  Then wait
+        // until this wave's copy of block kb+1 has landed and pass the barrier.
+        // Phase B: the 8 MFMAs of k step 1, the first P_LOADS followed by one DMA
+        // instruction of block kb+P_STAGES-1 (into the stage of block kb-1, whose
+        // reads were all consumed before this barrier) and the fragment reads of k
+        // step 0 of block kb+1.  Reads go in the order the MFMAs consume them;
+        // copies past the end repeat the last block into a free stage, so the loop
+        // has no branch.  sched_barrier(0) pins every slot.
+        static_assert(P_LOADS <= 8 && PFN == 2, "W8A8 schedule");
+        typedef unsigned v4u __attribute__((ext_vector_type(4)));
+        struct Frags { v4u fa[4], fb[2]; };
+        auto read_one = [&](int kb, int s2, int r, Frags& f) __attribute__((always_inline)) {
+            const uint8_t* la = plds + (kb % P_STAGES) * P_STAGE_BYTES;
+            const int c = 2 * s2 + fhalf;
+            if (r < 4) {
+                const int row = wm * 128 + r * 32 + frow;
+                f.fa[r] = *reinterpret_cast<const v4u*>(la + row * P_ROWB + swz(row, c) * 16);
+            } else {
+                const int row = wn * WTN_P + (r - 4) * 32 + frow;
+                f.fb[r - 4] = *reinterpret_cast<const v4u*>(la + P_BM * P_ROWB + row * P_ROWB + swz(row, c) * 16);
+            }
+        };
+        auto mfma_one = [&](const Frags& f, int t) __attribute__((always_inline)) {
+            const int i = t >> 1, j = t & 1;
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i, f.fb[j]),
+                                                             __builtin_bit_cast(v4i, f.fa[i]), acc[i][j], 0, 0, 0);
+        };
+        // reads after MFMA slot t: fb0 fa0 | fb1 | fa1 | fa2 | fa3
+        auto reads_after = [&](int t, int kb, int s2, Frags& f) __attribute__((always_inline)) {
+            if (t == 0) { read_one(kb, s2, 4, f); read_one(kb, s2, 0, f); }
+            if (t == 1) read_one(kb, s2, 5, f);
+            if (t == 2) read_one(kb, s2, 1, f);
+            if (t == 3) read_one(kb, s2, 2, f);
+            if (t == 4) read_one(kb, s2, 3, f);
+        };
+        auto dma_one = [&](int kb, int j) __attribute__((always_inline)) {
+            const uint32_t st = lds_base + (kb % P_STAGES) * P_STAGE_BYTES + wave * P_LOADS * 1024;
+            dma16(st + j * 1024, src[j] + min(kb, nkb - 1) * P_ROWB);
+        };
+        Frags F0, F1;
+#pragma unroll
+        for (int p = 0; p < P_STAGES - 1; ++p)
+#pragma unroll
+            for (int j = 0; j < P_LOADS; ++j) dma_one(p, j);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((P_STAGES - 2) * P_LOADS));   // block 0 landed
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < 6; ++r) read_one(0, 0, r, F0);
+        for (int kb = 0; kb < nkb; ++kb) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                mfma_one(F0, t);
+                __builtin_amdgcn_sched_barrier(0);
+                reads_after(t, kb, 1, F1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm((P_STAGES - 3) * P_LOADS));   // block kb+1 landed
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                mfma_one(F1, t);
+                __builtin_amdgcn_sched_barrier(0);
+                if (t < P_LOADS) dma_one(kb + P_STAGES - 1, t);
+                reads_after(t, kb + 1, 0, F0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));            // the copies past the end have landed
+    } else {
 #pragma unroll
     for (int p = 0; p < P_STAGES - 1; ++p)
         if (p < nkb) issue(p);
@@ -296,6 +369,7 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
                 for (int j = 0; j < PFN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b_hi[j], a_hi[i], acc[i][j], 0, 0, 0);
         }
+    }
     }
 
     __syncthreads();                                     // every wave is done with the stages
