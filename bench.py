@@ -80,7 +80,8 @@ class Linear:
         self.qw, self.ws = native.convrot_quant_int4(w, G)         # load-time weight quantization
         self.w6 = native.int4_to_bf6(self.qw)                        # load-time bf6 operand encoding
         self.qw8, self.ws8 = native.convrot_quant_int8(w, G)       # the int8 tier's weight
-        self.q8 = torch.empty((M_TOKENS, K), dtype=torch.int8, device=dev)
+        self.w8t = native.int8_to_i8t(self.qw8)                      # load-time I8T operand layout
+        self.q8 = torch.empty((native.i8t_rows(M_TOKENS), K), dtype=torch.int8, device=dev)
         self.bias = normal_bias(N, seed=seed + 2).to(dev).float()
         self.qx = torch.empty((M_TOKENS, K // 2), dtype=torch.int8, device=dev)
         self.a6 = torch.empty((native.bf6_rows(M_TOKENS), K // 4 * 3), dtype=torch.uint8, device=dev)
@@ -142,11 +143,11 @@ def main():
             calls.append(("gemm", i, lib.cr_int4_convrot_gemm_bf6,
                           (vp(L.a6.data_ptr()), vp(L.w6.data_ptr()), vp(L.xs.data_ptr()), vp(L.ws.data_ptr()),
                            vp(L.bias.data_ptr()), vp(L.out.data_ptr()), L.M, L.N, L.K, 1, sptr)))
-        elif args.path == "w8a8":
-            calls.append(("rq", i, lib.ck_convrot_quant_int8,
+        elif args.path == "w8a8":   # the int8 linear's path: I8T operands (K % 64 == 0)
+            calls.append(("rq", i, lib.cr_convrot_quant_int8_i8t,
                           (vp(L.x.data_ptr()), 1, vp(L.q8.data_ptr()), vp(L.xs.data_ptr()), L.M, L.K, G, sptr)))
-            calls.append(("gemm", i, lib.ck_int8_convrot_gemm,
-                          (vp(L.q8.data_ptr()), vp(L.qw8.data_ptr()), vp(L.xs.data_ptr()), vp(L.ws8.data_ptr()),
+            calls.append(("gemm", i, lib.cr_int8_convrot_gemm_i8t,
+                          (vp(L.q8.data_ptr()), vp(L.w8t.data_ptr()), vp(L.xs.data_ptr()), vp(L.ws8.data_ptr()),
                            vp(L.bias.data_ptr()), vp(L.out.data_ptr()), L.M, L.N, L.K, 1, sptr)))
         else:
             calls.append(("rq", i, lib.ck_convrot_quant_int4,
@@ -258,7 +259,7 @@ def main():
         "roofline": {
             "kernel": {"bf6": "w4a4_gemm_bf6_kernel<EPI_BF16> (v_mfma_scale_f32_32x32x64_f8f6f4, BF6 operands)",
                        "int8": "w4a4_gemm_pipe_kernel<EPI_BF16> (v_mfma_i32_32x32x32_i8, int4 unpacked)",
-                       "w8a8": "w4a4_gemm_pipe_kernel<EPI_BF16, I8> (v_mfma_i32_32x32x32_i8, int8 operands)"}[args.path],
+                       "w8a8": "w4a4_gemm_pipe_kernel<EPI_BF16, I8, I8T> (v_mfma_i32_32x32x32_i8, int8 operands in the I8T layout)"}[args.path],
             "bound": "mfma",
             "achieved": round(gemm_tops, 1),
             "peak": PEAK_FP6_TFLOPS if args.path == "bf6" else PEAK_INT8_TOPS,
@@ -269,7 +270,7 @@ def main():
         "rotate_quant": {
             "kernel": {"bf6": "rotquant_wave_kernel<bf16,256,3,B6T out>",
                        "int8": "rotquant_wave_kernel<bf16,256,3,packed int4 out>",
-                       "w8a8": "rotquant_wave_kernel<bf16,256,3,int8 out>"}[args.path],
+                       "w8a8": "rotquant_wave_kernel<bf16,256,3,I8T out>"}[args.path],
             "bound": "hbm",
             "GBps_at_M4608_K3072": round(metric_rq_gbs, 1),
             "frac_at_M4608_K3072": round(metric_rq_gbs / PEAK_HBM_GBS, 4),

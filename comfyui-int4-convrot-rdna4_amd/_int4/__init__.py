@@ -38,6 +38,8 @@ __all__ = [
     "MAX_LORA_RANK",
     "prepare_convrot_w4a4_weight_bf6",
     "bf6_path_ok",
+    "i8t_path_ok",
+    "prepare_convrot_w8a8_weight_i8t",
 ]
 
 # largest concatenated rank of the fused LoRA side path (padded to a multiple of 32)
@@ -156,6 +158,22 @@ def bf6_path_ok(in_features: int) -> bool:
     """True when a linear of this input width runs on the bf6 matrix-core GEMM
     (K % 128 == 0 and the fused quantizer covers K); others use the int8 GEMM."""
     return in_features % 128 == 0 and in_features <= native.max_quant_bf6_k()
+
+
+def i8t_path_ok(in_features: int) -> bool:
+    """True when a W8A8 linear of this input width runs on the tile-major (I8T)
+    int8 GEMM (K % 64 == 0 and the fused quantizer covers K); others use the
+    row-major int8 GEMM."""
+    return in_features % 64 == 0 and in_features <= native.max_quant_bf6_k()
+
+
+def prepare_convrot_w8a8_weight_i8t(qweight: torch.Tensor) -> torch.Tensor | None:
+    """Load-time re-layout of an int8 weight [N, K] into the I8T operand layout
+    of the W8A8 GEMM (int8 [ceil(N/256)*256, K], the same codes).  Returns None
+    when the weight's K cannot use that path."""
+    if not i8t_path_ok(qweight.shape[-1]):
+        return None
+    return native.int8_to_i8t(_on_gpu(qweight).contiguous())
 
 
 def prepare_convrot_w4a4_weight_bf6(qweight: torch.Tensor) -> torch.Tensor | None:
@@ -315,12 +333,18 @@ def convrot_w8a8_linear(
     wscales: torch.Tensor,
     bias: torch.Tensor | None = None,
     convrot_groupsize: int = 256,
+    *,
+    qweight_i8t: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Compute ``x @ W.T + bias`` with the gfx950 W8A8 ConvRot path (the int8
     tier, reference _int4/__init__.py:141-175): fused rotate + int8 quantize of
     x (the eager arithmetic of _int4/int8_eager.py:22-28), then the int8 GEMM
     with exact int32 accumulation and the fp32 epilogue, both on torch's current
-    stream.  qweight int8 [N, K], wscales [N] f32."""
+    stream.  qweight int8 [N, K], wscales [N] f32.  When K allows it the
+    activation is quantized straight into the tile-major I8T layout and the GEMM
+    reads ``qweight_i8t`` (from :func:`prepare_convrot_w8a8_weight_i8t`, made
+    once at load time; re-laid here when not given): the same codes and
+    accumulators, bit-identical outputs."""
     if x.shape[-1] != qweight.shape[-1]:
         raise ValueError(f"Input K={x.shape[-1]} does not match qweight K={qweight.shape[-1]}")
     if x.shape[-1] % convrot_groupsize != 0:
@@ -330,9 +354,16 @@ def convrot_w8a8_linear(
     x2d = x.reshape(-1, orig_shape[-1]).contiguous()
     if x2d.dtype not in native._IN_DTYPE_CODE:
         x2d = x2d.to(torch.float32)
-    qact, x_scale = native.convrot_quant_int8(x2d, convrot_groupsize)
     out_dtype = x.dtype if x.dtype in _NATIVE_OUT else torch.float32
-    out = native.int8_convrot_gemm(qact, qweight, x_scale, wscales, bias, out_dtype)
+    M, N = x2d.shape[0], qweight.shape[0]
+    if i8t_path_ok(x2d.shape[1]) and x2d.is_cuda:
+        w8t = qweight_i8t if qweight_i8t is not None else prepare_convrot_w8a8_weight_i8t(qweight)
+        a8t, x_scale = native.convrot_quant_int8_i8t(x2d, convrot_groupsize)
+        epi = native.EPI_F32 if out_dtype == torch.float32 else native.EPI_BF16
+        out = native.int8_convrot_gemm_i8t(a8t, w8t, x_scale, wscales, bias, epi, M, N)
+    else:
+        qact, x_scale = native.convrot_quant_int8(x2d, convrot_groupsize)
+        out = native.int8_convrot_gemm(qact, qweight, x_scale, wscales, bias, out_dtype)
     if out.dtype != x.dtype:
         out = out.to(x.dtype)
     return out.reshape(*orig_shape[:-1], qweight.shape[0])

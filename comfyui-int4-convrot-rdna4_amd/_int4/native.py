@@ -44,6 +44,9 @@ _SIGNATURES = {
     "ck_convrot_quant_int8": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
     "ck_int8_convrot_gemm": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
     "cr_int8_convrot_gemm_ex": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
+    "cr_convrot_quant_int8_i8t": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
+    "cr_int8_to_i8t": ([_vp, _vp, _i, _i, _vp], _i),
+    "cr_int8_convrot_gemm_i8t": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
     "cr_gemm_bf6_choose_nsplit": ([_i, _i, _i], _i),
     "cr_gemm_bf6_splitk_workspace": ([_i, _i, _i], ctypes.c_size_t),
     "cr_int4_convrot_gemm_bf6_splitk": ([_vp] * 7 + [_i, ctypes.c_float, _vp] + [_i] * 5 + [_vp, ctypes.c_size_t, _vp],
@@ -469,6 +472,75 @@ def int8_convrot_gemm(x_int8, w_int8, x_scale, w_scale, bias, out_dtype):
         raise ValueError(f"int8 gemm output dtype must be float32/bfloat16, got {out_dtype}")
     return int8_convrot_gemm_ex(x_int8, w_int8, x_scale, w_scale, bias,
                                 EPI_F32 if out_dtype == torch.float32 else EPI_BF16)
+
+
+def i8t_rows(rows: int) -> int:
+    """Rows of an I8T operand: the logical rows padded to a multiple of 256."""
+    return (rows + 255) // 256 * 256
+
+
+def int8_to_i8t(q: torch.Tensor) -> torch.Tensor:
+    """Row-major int8 codes [rows, K] -> the I8T operand of the W8A8 GEMM,
+    int8 [i8t_rows(rows), K] in chunk order (K % 64 == 0; padding rows zero)."""
+    lib = load_library()
+    _check_cuda(q)
+    if q.dtype != torch.int8 or q.dim() != 2:
+        raise ValueError("int8 codes must be a 2-D int8 tensor")
+    q = _aligned(q)
+    rows, K = q.shape
+    if K % 64 != 0:
+        raise ValueError(f"I8T operands need K % 64 == 0, got K={K}")
+    out = torch.empty((i8t_rows(rows), K), dtype=torch.int8, device=q.device)
+    rc = lib.cr_int8_to_i8t(_ptr(q), _ptr(out), rows, K, _stream(q.device))
+    if rc != 0:
+        raise RuntimeError(f"cr_int8_to_i8t failed, hipError={rc}")
+    return out
+
+
+def convrot_quant_int8_i8t(x: torch.Tensor, convrot_groupsize: int):
+    """Fused rotate + int8 quantize of x [M, K] straight into the I8T layout.
+    Returns (q int8 [i8t_rows(M), K], scale f32 [M]); the codes and scales equal
+    convrot_quant_int8's.  K % 64 == 0, K <= max_quant_bf6_k()."""
+    lib = load_library()
+    _check_cuda(x)
+    if x.dim() != 2 or x.dtype not in _IN_DTYPE_CODE:
+        raise ValueError("x must be a 2-D f32/bf16/f16 tensor")
+    if convrot_groupsize not in (16, 64, 256):
+        raise ValueError("fused convrot_quant_int8 supports groupsize 16/64/256")
+    x = _aligned(x)
+    M, K = x.shape
+    if K % 64 != 0 or K > lib.cr_max_quant_bf6_k() or K % convrot_groupsize != 0:
+        raise ValueError(f"I8T activation quantization needs K % 64 == 0 and K <= {lib.cr_max_quant_bf6_k()}")
+    q = torch.empty((i8t_rows(M), K), dtype=torch.int8, device=x.device)
+    s = torch.empty((M,), dtype=torch.float32, device=x.device)
+    rc = lib.cr_convrot_quant_int8_i8t(_ptr(x), _IN_DTYPE_CODE[x.dtype], _ptr(q), _ptr(s), M, K, convrot_groupsize,
+                                       _stream(x.device))
+    if rc != 0:
+        raise RuntimeError(f"cr_convrot_quant_int8_i8t failed, hipError={rc}")
+    return q, s
+
+
+def int8_convrot_gemm_i8t(a8t, w8t, x_scale, w_scale, bias, epilogue: int, M: int, N: int):
+    """W8A8 GEMM on I8T operands (a8t [i8t_rows(M), K], w8t [i8t_rows(N), K])
+    with epilogue 0 (f32), 1 (bf16) or 3 (int32 accumulators); bit-identical to
+    int8_convrot_gemm_ex on the row-major codes."""
+    lib = load_library()
+    _check_cuda(a8t, w8t, x_scale, w_scale, bias)
+    if a8t.dtype != torch.int8 or w8t.dtype != torch.int8:
+        raise ValueError("I8T operands must be int8")
+    K = a8t.shape[1]
+    if w8t.shape[1] != K or a8t.shape[0] != i8t_rows(M) or w8t.shape[0] != i8t_rows(N):
+        raise ValueError(f"I8T operand shapes {tuple(a8t.shape)} / {tuple(w8t.shape)} do not match M={M}, N={N}")
+    xs = x_scale.to(torch.float32).contiguous() if x_scale is not None else None
+    wsc = w_scale.to(torch.float32).contiguous() if w_scale is not None else None
+    b = bias.to(torch.float32).contiguous() if bias is not None else None
+    odt = {EPI_F32: torch.float32, EPI_BF16: torch.bfloat16, EPI_ACC: torch.int32}[epilogue]
+    out = torch.empty((M, N), dtype=odt, device=a8t.device)
+    rc = lib.cr_int8_convrot_gemm_i8t(_ptr(a8t), _ptr(w8t), _ptr(xs), _ptr(wsc), _ptr(b), _ptr(out),
+                                      M, N, K, epilogue, _stream(a8t.device))
+    if rc != 0:
+        raise RuntimeError(f"cr_int8_convrot_gemm_i8t failed, hipError={rc}")
+    return out
 
 
 def convrot_w4a4_linear_bf6(x2d, w6, w_scale, bias, down, up, scale: float, epilogue: int, convrot_groupsize: int,

@@ -47,6 +47,15 @@ __host__ __device__ __forceinline__ int b6_p_off(int r, int g) { return r * 64 +
 __host__ __device__ __forceinline__ int b6_q_off(int r, int g) {
     return B6_QOFF + ((r >> 6) * 32 + (r & 31)) * 64 + swz(r, g) * 16;
 }
+// The I8T operand layout of the W8A8 GEMM: an int8 matrix [rows, K] (K % 64 ==
+// 0, rows padded to a multiple of 256 with zero codes) as [rows/256][K/64]
+// chunks of 16384 bytes, each the GEMM's LDS stage image of that operand
+// block: row r at r*64, its 16-byte piece c (k = 64 kb + 16 c .. +15) at
+// swz(r, c)*16.  The GEMM then copies every chunk with contiguous 1 KB DMA
+// instructions.
+constexpr int I8T_CHUNK = 16384;
+__host__ __device__ __forceinline__ int i8t_off(int r, int c) { return r * 64 + swz(r, c) * 16; }
+
 // odd 32-row tiles keep dwords d0..d1 in the Q piece (its bytes 8..15)
 __host__ __device__ __forceinline__ bool b6_odd_tile(int r) { return ((r >> 5) & 1) != 0; }
 

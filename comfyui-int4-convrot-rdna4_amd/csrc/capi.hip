@@ -27,6 +27,11 @@ hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, cons
                            int bias_dt, const void* t, const void* U, int R, float scale, void* out, int M, int N,
                            int K, int epi, int nsplit, void* workspace, hipStream_t st);
 int gemm_bf6_choose_nsplit(int M, int N, int K);
+hipError_t rotquant_i8t_launch(const void* x, int in_dtype, int8_t* q, float* s, int M, int K, int G,
+                               hipStream_t st);
+hipError_t int8_to_i8t_launch(const void* src, void* dst, int rows, int K, hipStream_t st);
+hipError_t gemm_i8t_launch(const int8_t* X, const int8_t* W, const float* xs, const float* ws,
+                           const float* bias, void* out, int M, int N, int K, int epi, hipStream_t st);
 size_t gemm_bf6_splitk_workspace(int M, int N, int nsplit);
 }  // namespace convrot
 
@@ -185,6 +190,31 @@ API int ck_int8_convrot_gemm(const void* X, const void* W, const void* xscale, c
     return cr_int8_convrot_gemm_ex(X, W, xscale, wscale, bias, out, M, N, K, out_dtype, stream);
 }
 
+static int i8t_k_ok(int K) { return K > 0 && K % 64 == 0 && K < 131072; }
+
+API int cr_convrot_quant_int8_i8t(const void* x, int in_dtype, void* qout, void* scaleout, int M, int K, int G,
+                                  void* stream) {
+    if (!quant_args_ok(in_dtype, M, K, G) || !i8t_k_ok(K) || K > convrot::rotquant_b6_max_k()) return -1;
+    return (int)convrot::rotquant_i8t_launch(x, in_dtype, reinterpret_cast<int8_t*>(qout),
+                                             reinterpret_cast<float*>(scaleout), M, K, G,
+                                             reinterpret_cast<hipStream_t>(stream));
+}
+
+API int cr_int8_to_i8t(const void* src, void* dst, int rows, int K, void* stream) {
+    if (rows < 0 || !i8t_k_ok(K)) return -1;
+    return (int)convrot::int8_to_i8t_launch(src, dst, rows, K, reinterpret_cast<hipStream_t>(stream));
+}
+
+API int cr_int8_convrot_gemm_i8t(const void* X, const void* W, const void* xscale, const void* wscale,
+                                 const void* bias, void* out, int M, int N, int K, int epilogue, void* stream) {
+    if (!i8t_k_ok(K) || M < 0 || N < 0) return -1;
+    if (epilogue != 0 && epilogue != 1 && epilogue != 3) return -1;
+    return (int)convrot::gemm_i8t_launch(reinterpret_cast<const int8_t*>(X), reinterpret_cast<const int8_t*>(W),
+                                         reinterpret_cast<const float*>(xscale), reinterpret_cast<const float*>(wscale),
+                                         reinterpret_cast<const float*>(bias), out, M, N, K, epilogue,
+                                         reinterpret_cast<hipStream_t>(stream));
+}
+
 // ---------------------------------------------------------------------------
 // The whole bf6 linear in one call: rotate + quantize x into B6T, the LoRA down
 // projection (R > 0), the GEMM (k-split when the library chooses it) with the
@@ -238,4 +268,4 @@ API int cr_convrot_w4a4_linear_bf6(const void* x, int in_dtype, const void* W6, 
 
 API int cr_max_quant_k(void) { return convrot::rotquant_max_k(); }
 
-API int cr_abi_version(void) { return 5; }
+API int cr_abi_version(void) { return 6; }

@@ -188,7 +188,9 @@ constexpr int P_STAGES = CONVROT_PIPE_STAGES;
 constexpr int P_STAGE_BYTES = (P_BM + P_BN) * P_ROWB;  // 32 KB
 constexpr int P_LDS_BYTES = P_STAGES * P_STAGE_BYTES + EPI_SCALE_FLOATS * 4;
 
-template <int EPI, int WN, bool LORA, bool I8>
+// TM (W8A8 only): operands in the I8T layout (b6t_layout.h) instead of
+// row-major: each stage half is one contiguous 16 KB chunk.
+template <int EPI, int WN, bool LORA, bool I8, bool TM = false>
 __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
         const int8_t* __restrict__ Xp, const int8_t* __restrict__ Wp,
         const float* __restrict__ xs, const float* __restrict__ ws, const float* __restrict__ bias,
@@ -212,8 +214,14 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
     float* sc = reinterpret_cast<float*>(plds + P_STAGES * P_STAGE_BYTES);
     stage_scales(sc, xs, ws, bias, M, N, m0, n0, tid, 128 * WN);   // visible after the loop's first barrier
 
+    static_assert(!TM || (I8 && WN == 4), "I8T operands: W8A8, 8 waves");
     // DMA source rows / chunks for this lane's P_LOADS instructions (fixed per tile)
     const int8_t* src[P_LOADS];
+    if constexpr (TM) {   // waves 0..3 copy the A chunk, waves 4..7 the B chunk, 1 KB per instruction
+        const int8_t* base = wave < 4 ? Xp + (size_t)tm * nkb * I8T_CHUNK : Wp + (size_t)tn * nkb * I8T_CHUNK;
+#pragma unroll
+        for (int j = 0; j < P_LOADS; ++j) src[j] = base + ((wave & 3) * P_LOADS + j) * 1024 + lane * 16;
+    } else
 #pragma unroll
     for (int j = 0; j < P_LOADS; ++j) {
         const int slot = (wave * P_LOADS + j) * 64 + lane;   // 16-byte slot of the stage
@@ -283,7 +291,7 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
         };
         auto dma_one = [&](int kb, int j) __attribute__((always_inline)) {
             const uint32_t st = lds_base + (kb % P_STAGES) * P_STAGE_BYTES + wave * P_LOADS * 1024;
-            dma16(st + j * 1024, src[j] + min(kb, nkb - 1) * P_ROWB);
+            dma16(st + j * 1024, src[j] + (size_t)min(kb, nkb - 1) * (TM ? I8T_CHUNK : P_ROWB));
         };
         Frags F0, F1;
 #pragma unroll
@@ -378,11 +386,11 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
                                          n0 + wn * WTN_P, lane, lora, plds + wave * SCR);
 }
 
-template <int EPI, bool LORA, bool I8 = false>
+template <int EPI, bool LORA, bool I8 = false, bool TM = false>
 static hipError_t launch_epi(const int8_t* Xp, const int8_t* Wp, const float* xs, const float* ws,
                              const float* bias, void* out, int M, int N, int K, const LoraArgs& la,
                              hipStream_t st) {
-    if ((I8 ? K : K / 2) % P_ROWB == 0) {
+    if (TM || (I8 ? K : K / 2) % P_ROWB == 0) {
         constexpr int WN = CONVROT_PIPE_WN;
         const int ntiles = ((M + P_BM - 1) / P_BM) * ((N + P_BN - 1) / P_BN);
         constexpr int kMaxDev = 64;
@@ -392,15 +400,15 @@ static hipError_t launch_epi(const int8_t* Xp, const int8_t* Wp, const float* xs
         if (e != hipSuccess) return e;
         if (dev < 0 || dev >= kMaxDev) return hipErrorInvalidDevice;
         if (!attr_set[dev]) {
-            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_pipe_kernel<EPI, WN, LORA, I8>),
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_pipe_kernel<EPI, WN, LORA, I8, TM>),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, P_LDS_BYTES);
             if (e != hipSuccess) return e;
             attr_set[dev] = true;
         }
-        hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<EPI, WN, LORA, I8>), dim3(ntiles), dim3(128 * WN),
+        hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<EPI, WN, LORA, I8, TM>), dim3(ntiles), dim3(128 * WN),
                            P_LDS_BYTES, st, Xp, Wp, xs, ws, bias, out, M, N, K, la,
                            tile_group_rows((M + P_BM - 1) / P_BM));
-    } else {
+    } else if constexpr (!TM) {
         dim3 grid((N + TBN - 1) / TBN, (M + TBM - 1) / TBM), block(NTHR);
         hipLaunchKernelGGL((w4a4_gemm_kernel<EPI, LORA, I8>), grid, block, 0, st, Xp, Wp, xs, ws, bias, out, M, N, K, la);
     }
@@ -432,6 +440,46 @@ hipError_t gemm_i8_launch(const int8_t* X, const int8_t* W, const float* xs, con
         case EPI_ACC: return launch_epi<EPI_ACC, false, true>(X, W, xs, ws, bias, out, M, N, K, none, st);
         default: return hipErrorInvalidValue;
     }
+}
+
+// W8A8 GEMM on I8T operands (K % 64 == 0; rows of A and W padded to 256)
+hipError_t gemm_i8t_launch(const int8_t* X, const int8_t* W, const float* xs, const float* ws,
+                           const float* bias, void* out, int M, int N, int K, int epi, hipStream_t st) {
+    if (M == 0 || N == 0) return hipSuccess;
+    if (K % 64 != 0) return hipErrorInvalidValue;
+    const LoraArgs none{nullptr, nullptr, 0, 0.0f};
+    switch (epi) {
+        case EPI_F32: return launch_epi<EPI_F32, false, true, true>(X, W, xs, ws, bias, out, M, N, K, none, st);
+        case EPI_BF16: return launch_epi<EPI_BF16, false, true, true>(X, W, xs, ws, bias, out, M, N, K, none, st);
+        case EPI_ACC: return launch_epi<EPI_ACC, false, true, true>(X, W, xs, ws, bias, out, M, N, K, none, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// row-major int8 [rows, K] -> I8T (K % 64 == 0); one thread per 16-byte piece
+// of the padded matrix, consecutive threads on the pieces of consecutive rows
+__global__ __launch_bounds__(256) void int8_to_i8t_kernel(const int8_t* __restrict__ src, int8_t* __restrict__ dst,
+                                                          int rows, int K) {
+    const int nkb = K / 64;
+    const long long id = (long long)blockIdx.x * 256 + threadIdx.x;
+    const int tiles = (rows + 255) / 256;
+    if (id >= (long long)tiles * nkb * 1024) return;
+    const int c = (int)(id & 3), r = (int)((id >> 2) & 255);
+    const long long tk = id >> 10;                       // tile * nkb + kb
+    const int tile = (int)(tk / nkb), kb = (int)(tk % nkb);
+    const int row = tile * 256 + r;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (row < rows) v = *reinterpret_cast<const uint4*>(src + (size_t)row * K + kb * 64 + c * 16);
+    *reinterpret_cast<uint4*>(dst + (size_t)tk * I8T_CHUNK + i8t_off(r, c)) = v;
+}
+
+hipError_t int8_to_i8t_launch(const void* src, void* dst, int rows, int K, hipStream_t st) {
+    if (rows < 0 || K <= 0 || K % 64 != 0) return hipErrorInvalidValue;
+    if (rows == 0) return hipSuccess;
+    const long long threads = (long long)((rows + 255) / 256) * (K / 64) * 1024;
+    hipLaunchKernelGGL(int8_to_i8t_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                       reinterpret_cast<const int8_t*>(src), reinterpret_cast<int8_t*>(dst), rows, K);
+    return hipGetLastError();
 }
 
 hipError_t gemm_lora_launch(const int8_t* Xp, const int8_t* Wp, const float* xs, const float* ws,

@@ -390,7 +390,9 @@ __device__ __forceinline__ void b6_store_group(int8_t* out, int row, int K, int 
 // layout of the bf6 GEMM (b6t_layout.h; K % 128 == 0; rows M .. ceil(M/256)*256
 // get zero codes); OUT_I8 the int8 tier's plain int8 codes (scale a / 127,
 // codes clamped to [-127, 127], _int4/int8_eager.py:22-28).
-enum : int { OUT_PACK4 = 0, OUT_B6T = 1, OUT_I8 = 2 };
+// OUT_I8T the same int8 codes in the I8T layout of the W8A8 GEMM (b6t_layout.h;
+// K % 64 == 0; padding rows get zero codes).
+enum : int { OUT_PACK4 = 0, OUT_B6T = 1, OUT_I8 = 2, OUT_I8T = 3 };
 
 template <int DT, int G, int NPMAX, int OUT>
 __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
@@ -420,7 +422,8 @@ __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
     const int gl = lane % LPG;
     const int gfirst = lane - gl;
     const float kMagic = 12582912.0f;
-    constexpr float QMAX = OUT == OUT_I8 ? 127.0f : 7.0f;
+    constexpr bool INT8 = OUT == OUT_I8 || OUT == OUT_I8T;
+    constexpr float QMAX = INT8 ? 127.0f : 7.0f;
 
     ChunkRegs<DT> nxt;
     int row = blockIdx.x * kWaves + wv;
@@ -509,7 +512,7 @@ __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
                                                         bf16hi_to_f32(hv[p].w[i >> 1]) * rinv32);
                         z0 = bf16lo_to_f32(zz);
                         z1 = bf16hi_to_f32(zz);
-                        if constexpr (OUT == OUT_I8) {
+                        if constexpr (INT8) {
                             z0 = fminf(fmaxf(z0, -QMAX), QMAX);
                             z1 = fminf(fmaxf(z1, -QMAX), QMAX);
                         }
@@ -554,6 +557,10 @@ __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
                 wave_sync();
                 if (OUT == OUT_I8 && ok) {
                     *reinterpret_cast<uint4*>(qout + (size_t)row * K + (size_t)c * kChunk) = w;
+                } else if (OUT == OUT_I8T && ok) {
+                    const int k0 = c * kChunk;
+                    int8_t* chunk = qout + ((size_t)(row >> 8) * (K >> 6) + (k0 >> 6)) * I8T_CHUNK;
+                    *reinterpret_cast<uint4*>(chunk + i8t_off(row & 255, (k0 >> 4) & 3)) = w;
                 } else if (B6 && ok) {
                     // chunks (2g', 2g'+1) are the 32 codes of one MFMA group: the even lane
                     // converts them (bf16 values, element order) with the 32-wide BF6
@@ -580,6 +587,14 @@ __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
                 }
             }
         }
+    }
+    if constexpr (OUT == OUT_I8T) {   // zero codes in the padding rows of the last 256-row tile
+        const int mpad = (M + 255) & ~255;
+        for (int prow = M + blockIdx.x * kWaves + wv; prow < mpad; prow += nwaves)
+            for (int k0 = 16 * lane; k0 < K; k0 += 16 * 64) {
+                int8_t* chunk = qout + ((size_t)(prow >> 8) * (K >> 6) + (k0 >> 6)) * I8T_CHUNK;
+                *reinterpret_cast<uint4*>(chunk + i8t_off(prow & 255, (k0 >> 4) & 3)) = make_uint4(0u, 0u, 0u, 0u);
+            }
     }
     if constexpr (B6) {   // zero codes in the padding rows of the last 256-row tile
         const int mpad = (M + 255) & ~255;
@@ -716,6 +731,26 @@ hipError_t rotquant_b6_launch(const void* x, int in_dtype, uint8_t* a6, float* s
 }
 
 int rotquant_b6_max_k() { return kWaveMaxK; }
+
+// fused rotate + int8 quantize into the I8T layout (K % 64 == 0, K <= 12288)
+hipError_t rotquant_i8t_launch(const void* x, int in_dtype, int8_t* q, float* s, int M, int K, int G,
+                               hipStream_t st) {
+    if (K % 64 != 0 || K > kWaveMaxK || M < 0) return hipErrorInvalidValue;
+#define RI8T_G(DT)                                                                                  \
+    switch (G) {                                                                                    \
+        case 16: return rq_wave_launch<DT, 16, OUT_I8T>(x, q, s, M, K, st);                         \
+        case 64: return rq_wave_launch<DT, 64, OUT_I8T>(x, q, s, M, K, st);                         \
+        case 256: return rq_wave_launch<DT, 256, OUT_I8T>(x, q, s, M, K, st);                       \
+        default: return hipErrorInvalidValue;                                                       \
+    }
+    switch (in_dtype) {
+        case DT_F32: RI8T_G(DT_F32)
+        case DT_BF16: RI8T_G(DT_BF16)
+        case DT_F16: RI8T_G(DT_F16)
+        default: return hipErrorInvalidValue;
+    }
+#undef RI8T_G
+}
 
 // fused rotate + int8 quantize (W8A8 activations / weights): plain int8 [M, K]
 hipError_t rotquant_i8_launch(const void* x, int in_dtype, int8_t* q, float* s, int M, int K, int G,

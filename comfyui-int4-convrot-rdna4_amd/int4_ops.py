@@ -142,6 +142,7 @@ if _COMFY_OPS and _CK_OK:
                 self._qgs = None      # convrot groupsize
                 self._qmode = None    # "int4" | "int8" | None (bf16)
                 self._q6 = None       # int4 weight re-encoded for the bf6 matrix-core GEMM (load time)
+                self._q8t = None      # int8 weight re-laid for the tile-major W8A8 GEMM (load time)
                 self._dyn_lora = None
                 self._dyn_fused = None   # (D, U) bf16: plain LoRAs fused into the GEMM epilogue
                 self._dyn_rest = None    # adapters that keep the generic h() side path
@@ -304,6 +305,7 @@ if _COMFY_OPS and _CK_OK:
                 self._qs = state_dict[skey].to(dev, torch.float32).reshape(-1).contiguous()
                 self._qgs, self._qmode = gs, mode
                 self._q6 = _ck.prepare_convrot_w4a4_weight_bf6(self._q) if mode == "int4" else None
+                self._q8t = _ck.prepare_convrot_w8a8_weight_i8t(self._q) if mode == "int8" else None
                 self.weight = None
                 for k in (wkey, skey, qkey):
                     state_dict.pop(k, None)
@@ -366,6 +368,7 @@ if _COMFY_OPS and _CK_OK:
                                 w.to(dev, torch.float16), convrot_groupsize=gs, stochastic_rounding=stoch)
                         self._q, self._qs, self._qgs, self._qmode = qw, ws.float(), gs, mode
                         self._q6 = _ck.prepare_convrot_w4a4_weight_bf6(qw) if mode == "int4" else None
+                        self._q8t = _ck.prepare_convrot_w8a8_weight_i8t(qw) if mode == "int8" else None
                         self.weight = None
                         state_dict.pop(wkey, None)
                         self._take_bias(state_dict, prefix, dev)
@@ -385,12 +388,14 @@ if _COMFY_OPS and _CK_OK:
                     self._qs = self._qs.to(x.device)
                     if self._q6 is not None:
                         self._q6 = self._q6.to(x.device)
+                    if self._q8t is not None:
+                        self._q8t = self._q8t.to(x.device)
                 bias = self.bias
                 if bias is not None and bias.device != x.device:
                     bias = bias.to(x.device)
                 if self._qmode == "int8":
                     out = _ck.convrot_w8a8_linear(x, self._q, self._qs, bias=bias,
-                                                  convrot_groupsize=self._qgs)
+                                                  convrot_groupsize=self._qgs, qweight_i8t=self._q8t)
                     return self._apply_dyn_lora(x, out)
                 fused = self._dyn_fused
                 if fused is not None and fused[0].device != x.device:

@@ -223,6 +223,26 @@ int ck_int8_convrot_gemm(const void* X, const void* W, const void* xscale, const
 int cr_int8_convrot_gemm_ex(const void* X, const void* W, const void* xscale, const void* wscale,
                             const void* bias, void* out, int M, int N, int K, int epilogue, void* stream);
 
+/*
+ * The W8A8 tier on the I8T operand layout (no counterpart in the reference: a
+ * gfx950 layout of the same int8 codes).  An int8 matrix [rows, K], K % 64 == 0,
+ * is stored as ceil(rows/256) x K/64 chunks of 16384 bytes, the rows padded
+ * with zero codes: chunk (t, kb) holds rows 256t..256t+255, k = 64kb..64kb+63,
+ * row r at byte r*64, its 16-byte piece c at (c ^ f(r))*16 with
+ * f(r) = (((r >> 1) ^ (r >> 3)) & 1) | ((r >> 1) & 2).  Size: ceil(rows/256)*256*K.
+ *
+ * cr_convrot_quant_int8_i8t: ck_convrot_quant_int8 (same codes and scales, the
+ *   reference _int4/int4_gemm.hip:664-676 path) written in I8T; K <= cr_max_quant_bf6_k().
+ * cr_int8_to_i8t: re-lays row-major int8 codes (a quantized weight) into I8T.
+ * cr_int8_convrot_gemm_i8t: cr_int8_convrot_gemm_ex on I8T operands; the
+ *   accumulators and outputs equal the row-major call's bit for bit.
+ */
+int cr_convrot_quant_int8_i8t(const void* x, int in_dtype, void* qout, void* scaleout, int M, int K, int G,
+                              void* stream);
+int cr_int8_to_i8t(const void* src, void* dst, int rows, int K, void* stream);
+int cr_int8_convrot_gemm_i8t(const void* X, const void* W, const void* xscale, const void* wscale,
+                             const void* bias, void* out, int M, int N, int K, int epilogue, void* stream);
+
 /* Largest K accepted by the quantization entry points. */
 int cr_max_quant_k(void);
 

@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol(native):
 
 def test_library_queries_without_gpu(native):
     lib = native.load_library()
-    assert lib.cr_abi_version() == 5
+    assert lib.cr_abi_version() == 6
     assert lib.cr_max_quant_k() == 32768
     assert lib.cr_max_quant_bf6_k() == 12288
 
@@ -78,6 +78,12 @@ def test_argument_errors_return_minus_one(native):
     assert lib.ck_int8_convrot_gemm(n, n, n, n, n, n, 4, 4, 40, 1, n) == -1  # K % 16
     assert lib.ck_int8_convrot_gemm(n, n, n, n, n, n, 4, 4, 64, 2, n) == -1  # out dtype
     assert lib.cr_int8_convrot_gemm_ex(n, n, n, n, n, n, 4, 4, 64, 2, n) == -1  # no eager bf16 chain for int8
+    assert lib.cr_convrot_quant_int8_i8t(n, 1, n, n, 4, 160, 16, n) == -1      # K % 64
+    assert lib.cr_convrot_quant_int8_i8t(n, 1, n, n, 4, 16384, 256, n) == -1   # above the wave quantizer's K
+    assert lib.cr_int8_to_i8t(n, n, 4, 96, n) == -1                             # K % 64
+    assert lib.cr_int8_to_i8t(n, n, -1, 64, n) == -1                            # rows < 0
+    assert lib.cr_int8_convrot_gemm_i8t(n, n, n, n, n, n, 4, 4, 96, 1, n) == -1  # K % 64
+    assert lib.cr_int8_convrot_gemm_i8t(n, n, n, n, n, n, 4, 4, 64, 2, n) == -1  # no eager bf16 chain
     sk = lib.cr_int4_convrot_gemm_bf6_splitk
     assert sk(n, n, n, n, n, n, n, 0, f, n, 4, 4, 256, 0, 0, n, 0, n) == -1        # nsplit < 1
     assert sk(n, n, n, n, n, n, n, 0, f, n, 4, 4, 256, 0, 3, n, 1 << 30, n) == -1  # more splits than 128-k blocks

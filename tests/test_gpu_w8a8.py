@@ -174,6 +174,95 @@ def _ops():
     return m.Int4ConvRotOps
 
 
+# ---------------------------------------------------------------------------
+# I8T: the tile-major int8 operand layout of the W8A8 GEMM (the linear's path
+# when K % 64 == 0)
+# ---------------------------------------------------------------------------
+
+def i8t_np(q):
+    """Host re-layout of int8 codes [rows, K] into I8T, written from the layout's
+    definition: [ceil(rows/256)][K/64] chunks of 256 rows x 64 bytes, row r at
+    r*64, its 16-byte piece c at (c ^ f(r))*16, padding rows zero."""
+    rows, K = q.shape
+    tiles, nkb = (rows + 255) // 256, K // 64
+    qp = np.zeros((tiles * 256, K), dtype=np.int8)
+    qp[:rows] = q
+    qt = qp.reshape(tiles, 256, nkb, 4, 16).transpose(0, 2, 1, 3, 4)        # [t, kb, r, c, 16]
+    r = np.arange(256)
+    f = (((r >> 1) ^ (r >> 3)) & 1) | ((r >> 1) & 2)
+    idx = np.arange(4)[None, :] ^ f[:, None]                                  # slot p holds piece p ^ f(r)
+    out = np.take_along_axis(qt, idx[None, None, :, :, None], axis=3)
+    return out.reshape(tiles * 256, K)
+
+
+I8T_QUANT_CASES = [(1, 256, 256, torch.bfloat16), (33, 192, 64, torch.bfloat16), (300, 3072, 256, torch.bfloat16),
+                   (257, 12288, 256, torch.bfloat16), (65, 3072, 256, torch.float16), (17, 512, 64, torch.float32),
+                   (8, 64, 16, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("M,K,G,dt", I8T_QUANT_CASES)
+def test_quant_int8_i8t_layout(native, gpu, M, K, G, dt):
+    x = outlier_activations(M, K, seed=M + K, dtype=dt).cuda()
+    q, s = native.convrot_quant_int8(x, G)
+    q8t, s8t = native.convrot_quant_int8_i8t(x, G)
+    assert torch.equal(s8t, s)
+    want = i8t_np(q.cpu().numpy())
+    assert np.array_equal(q8t.cpu().numpy(), want)
+    assert np.array_equal(native.int8_to_i8t(q).cpu().numpy(), want)
+
+
+I8T_GEMM_SHAPES = [(64, 48, 256), (257, 300, 3072), (33, 513, 1088), (512, 256, 64), (300, 700, 12288)]
+
+
+@pytest.mark.parametrize("M,N,K", I8T_GEMM_SHAPES)
+def test_int8_i8t_gemm_bitexact(native, oracle, gpu, M, N, K):
+    rs = np.random.RandomState(7 * M + N + K)
+    X = rs.randint(-128, 128, size=(M, K)).astype(np.int8)
+    W = rs.randint(-128, 128, size=(N, K)).astype(np.int8)
+    xs = rs.uniform(0.005, 0.05, size=M).astype(np.float32)
+    ws = rs.uniform(0.005, 0.05, size=N).astype(np.float32)
+    b = (rs.standard_normal(N) * 0.01).astype(np.float32)
+    a8t, w8t = native.int8_to_i8t(cu(X)), native.int8_to_i8t(cu(W))
+    acc = oracle.int8_gemm(X, W)
+    got = native.int8_convrot_gemm_i8t(a8t, w8t, None, None, None, native.EPI_ACC, M, N).cpu().numpy()
+    assert np.array_equal(got, acc)
+    f32 = native.int8_convrot_gemm_i8t(a8t, w8t, cu(xs), cu(ws), cu(b), native.EPI_F32, M, N).cpu().numpy()
+    assert np.array_equal(f32.view(np.uint32), oracle.epilogue_f32(acc, xs, ws, b).view(np.uint32))
+    bf = np_of(native.int8_convrot_gemm_i8t(a8t, w8t, cu(xs), cu(ws), None, native.EPI_BF16, M, N))
+    assert np.array_equal(bf, oracle.epilogue_f32(acc, xs, ws, None, out_bf16=True))
+
+
+def test_int8_i8t_gemm_full_size_matches_row_major(native, gpu):
+    M, N, K = 4608, 3072, 3072
+    g = torch.Generator(device="cuda").manual_seed(6)
+    X = torch.randint(-127, 128, (M, K), generator=g, device="cuda", dtype=torch.int8)
+    W = torch.randint(-127, 128, (N, K), generator=g, device="cuda", dtype=torch.int8)
+    xs = torch.rand(M, generator=g, device="cuda") * 0.01
+    ws = torch.rand(N, generator=g, device="cuda") * 0.01
+    b = torch.rand(N, generator=g, device="cuda") * 0.01
+    ref = native.int8_convrot_gemm(X, W, xs, ws, b, torch.bfloat16)
+    got = native.int8_convrot_gemm_i8t(native.int8_to_i8t(X), native.int8_to_i8t(W), xs, ws, b,
+                                       native.EPI_BF16, M, N)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+def test_linear_w8a8_i8t_and_row_major_paths_agree(backend, native, gpu):
+    """K % 64 == 0 takes the I8T path; the same linear through the row-major
+    kernels gives the same bits."""
+    M, N, K = 129, 384, 3072
+    x = outlier_activations(M, K, seed=61).cuda()
+    w = normal_weight(N, K, seed=62, dtype=torch.float16).cuda()
+    b = normal_bias(N, seed=63).cuda()
+    int8_eager = importlib.import_module("comfyui-int4-convrot-rdna4_amd._int4.int8_eager")
+    qw, ws = int8_eager.quantize_convrot_w8a8_weight(w, 256)
+    assert backend.i8t_path_ok(K)
+    y = backend.convrot_w8a8_linear(x, qw, ws, bias=b, convrot_groupsize=256,
+                                    qweight_i8t=backend.prepare_convrot_w8a8_weight_i8t(qw))
+    qa, xs = native.convrot_quant_int8(x, 256)
+    ref = native.int8_convrot_gemm(qa, qw, xs, ws, b, torch.bfloat16)
+    assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+
+
 def test_ops_int8_layer_quantized_on_load(backend, oracle, gpu):
     Ops = _ops()
     M, N, K = 96, 640, 3072
@@ -192,6 +281,7 @@ def test_ops_int8_layer_quantized_on_load(backend, oracle, gpu):
     assert lin._qmode == "int4"
     m = parent.blk.lin
     assert m._qmode == "int8" and m._q.shape == (N, K) and m._q.dtype == torch.int8 and m._q6 is None
+    assert m._q8t is not None and m._q8t.shape == ((N + 255) // 256 * 256, K)
     qw, ws = oracle.quantize_weight8(np_of(w.to(torch.float16)), oracle.F16, 256)
     assert np.array_equal(m._q.cpu().numpy(), qw) and np.array_equal(m._qs.cpu().numpy(), ws)
     x = outlier_activations(M, K, seed=43)
