@@ -271,19 +271,25 @@ __global__ __launch_bounds__(kMaxThreads) void rotquant_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Wave-per-row kernel (no workgroup barriers).
+// Row-split kernel (K <= 12288).
 //
-// Each 64-lane wave owns whole rows and walks them persistently
-// (row = global wave id, += number of waves).  A row of K elements is
-// K/16 chunks handled in np = ceil(K/1024) passes of 64 lanes; the chunk of
-// the next pass (or of the next row's first pass) is loaded while the current
-// one is computed.  The fp64 transpose and the code gather use a private LDS
-// region per wave, so lanes only synchronise with their own wave, and the row
-// absmax is a shuffle reduction.  Rounded rotated values stay in registers as
-// packed 16-bit pairs until the row scale is known.
+// A workgroup of W waves quantizes one row at a time and walks rows
+// persistently (blockIdx.x, + gridDim.x, ...).  A row of K elements is K/16
+// chunks; wave w of the workgroup rotates chunks (p * W + w) * 64 + lane for
+// the passes p < P, so W * P passes of 64 lanes cover the row.  While a row is
+// rotated, every wave already loads its chunks of the workgroup's next row.
+// The fp64 transpose and the code gather use a private LDS region per wave;
+// the row absmax is a shuffle reduction within each wave and then a max over
+// the W waves through LDS, the workgroup's one barrier per row.  Rounded
+// rotated values stay in registers as packed 16-bit pairs until the row scale
+// is known.  Splitting rows over the waves of a workgroup keeps every wave's
+// share of the work small, so the last rows of the launch do not leave a few
+// waves running a whole row each while the rest of the chip idles.
 // ---------------------------------------------------------------------------
 
-constexpr int kWaves = 4;      // independent waves per workgroup
+constexpr int kRowMaxWaves = 4;                        // waves per workgroup
+constexpr int kRowMaxPass = 3;                         // passes per wave
+constexpr int kRowWaveLds = 64 * kPad * 8;             // LDS bytes per wave
 
 typedef unsigned v16u __attribute__((ext_vector_type(16)));
 typedef unsigned v6u __attribute__((ext_vector_type(6)));
@@ -394,204 +400,281 @@ __device__ __forceinline__ void b6_store_group(int8_t* out, int row, int K, int 
 // K % 64 == 0; padding rows get zero codes).
 enum : int { OUT_PACK4 = 0, OUT_B6T = 1, OUT_I8 = 2, OUT_I8T = 3 };
 
-template <int DT, int G, int NPMAX, int OUT>
-__global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
+// all butterfly stages of one chunk (16 values of the lane in v); tbuf is the
+// wave's transpose buffer
+template <int G>
+__device__ __forceinline__ void rotate_chunk(double (&v)[16], double* tbuf, int lane, int gl, int gfirst) {
+    if constexpr (G == 16) {
+        stage16<1>(v, 1.0);
+        stage16<4>(v, 0.25);
+    } else {
+        stage16<1>(v, 1.0);
+        stage16<4>(v, 1.0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) tbuf[lane * kPad + i] = v[i];
+        wave_sync();
+        if constexpr (G == 256) {
+#pragma unroll
+            for (int m = 0; m < 16; ++m) v[m] = tbuf[(gfirst + m) * kPad + gl];
+            stage16<1>(v, 1.0);
+            stage16<4>(v, 1.0 / 16.0);
+        } else {
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+#pragma unroll
+                for (int a = 0; a < 4; ++a) v[a + 4 * b] = tbuf[(gfirst + b) * kPad + 4 * gl + a];
+            stage16<4>(v, 1.0 / 8.0);
+        }
+        wave_sync();
+    }
+}
+
+// max(m, |a|, |b|) in one instruction
+__device__ __forceinline__ float absmax3(float m, float a, float b) {
+    float r;
+    asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+    return r;
+}
+
+// round the 16 rotated values to DT, keep them in h and fold them into lmax
+template <int DT>
+__device__ __forceinline__ void hold_chunk(const double (&v)[16], Held<DT>& h, float& lmax) {
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+        if constexpr (DT == DT_BF16) {
+            // lmax gathers jammed values: its RNE is the max of the rounded values
+            const float f0 = jam_to_f32(v[i]), f1 = jam_to_f32(v[i + 1]);
+            h.w[i >> 1] = pack_bf16x2(f0, f1);
+            lmax = absmax3(lmax, f0, f1);
+        } else {
+            const float r0 = round_f64_to_dt<DT>(v[i]);
+            const float r1 = round_f64_to_dt<DT>(v[i + 1]);
+            hold<DT>(h, i, r0, r1);
+            lmax = absmax3(lmax, r0, r1);
+        }
+    }
+}
+
+// max(v, v of another lane) on the bit patterns of non-negative floats (the
+// integer order of such patterns is their float order), the other lane chosen
+// by the DPP control CTRL on the rows in ROW_MASK (other rows take 0: keep v)
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t umax_dpp(uint32_t v) {
+    const uint32_t t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, false);
+    return v > t ? v : t;
+}
+
+// max over the 64 lanes of a non-negative, non-NaN float, as a wave-uniform value
+__device__ __forceinline__ float wave_max_nonneg(float f) {
+    uint32_t v = __float_as_uint(f);
+    v = umax_dpp<0xb1, 0xf>(v);     // quad_perm [1,0,3,2]
+    v = umax_dpp<0x4e, 0xf>(v);     // quad_perm [2,3,0,1]
+    v = umax_dpp<0x124, 0xf>(v);    // row_ror:4
+    v = umax_dpp<0x128, 0xf>(v);    // row_ror:8: every lane holds its row's max
+    v = umax_dpp<0x142, 0xa>(v);    // row_bcast:15 into rows 1 and 3
+    v = umax_dpp<0x143, 0xc>(v);    // row_bcast:31 into rows 2 and 3: lane 63 holds the max
+    return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)v, 63));
+}
+
+// max(a, b, c) in one instruction (no NaN operands here)
+__device__ __forceinline__ float fmax3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+template <int DT, int G, int P, int OUT>
+__global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
         const void* __restrict__ x, int8_t* __restrict__ qout, float* __restrict__ sout, int M, int K) {
     constexpr int LPG = G / kChunk;
     constexpr bool B6 = OUT == OUT_B6T;
-    // Per-wave LDS: the fp64 transpose buffer of the rotation passes, reused as
-    // the code reorder buffer of the quantize loop (which runs after every pass
-    // of the row; a wave's LDS operations complete in order).  Codes: bytes (64
+    constexpr bool INT8 = OUT == OUT_I8 || OUT == OUT_I8T;
+    constexpr float QMAX = INT8 ? 127.0f : 7.0f;
+    // Per-wave LDS: the fp64 transpose buffer of the rotation, reused as the
+    // code reorder buffer of the quantize loop (which runs after every pass of
+    // the row; a wave's LDS operations complete in order).  Codes: bytes (64
     // chunks x 16) for the integer outputs; for B6T the rounded codes as bf16,
     // chunk ch at (ch / 16) * 544 + (ch % 16) * 32 bytes (the pad spreads the
-    // four 16-lane groups over the banks).  One buffer keeps 4 workgroups per CU.
+    // four 16-lane groups over the banks).  After the W wave buffers: the
+    // per-wave row absmax, 8 slots per row parity (slots W..7 hold zeros).
     constexpr int kB6Group = 544;
-    __shared__ __attribute__((aligned(16))) double tbuf_all[kWaves][64 * kPad];
-    static_assert(64 * kPad * 8 >= (B6 ? 4 * kB6Group : 64 * 16), "code buffer");
+    static_assert(kRowWaveLds >= (B6 ? 4 * kB6Group : 64 * 16), "code buffer");
+    extern __shared__ __attribute__((aligned(16))) double rq_lds[];
 
+    const int W = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: rows are per wave
-    double* tbuf = tbuf_all[wv];
-    uint8_t* cb = reinterpret_cast<uint8_t*>(tbuf_all[wv]);
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    double* tbuf = rq_lds + wv * (64 * kPad);
+    uint8_t* cb = reinterpret_cast<uint8_t*>(tbuf);
+    float* red = reinterpret_cast<float*>(rq_lds + W * (64 * kPad));
     auto b6_slot = [&](int ch, int pos) {
         return reinterpret_cast<uint16_t*>(cb + (ch >> 4) * kB6Group + (ch & 15) * 32) + pos;
     };
-    const int nwaves = gridDim.x * kWaves;
     const int nchunks = K / kChunk;
-    const int np = (nchunks + 63) >> 6;
     const int gl = lane % LPG;
     const int gfirst = lane - gl;
     const float kMagic = 12582912.0f;
-    constexpr bool INT8 = OUT == OUT_I8 || OUT == OUT_I8T;
-    constexpr float QMAX = INT8 ? 127.0f : 7.0f;
+    if (wv == 0 && lane < 16 && (lane & 7) >= W) red[lane] = 0.0f;   // before the first barrier
 
-    ChunkRegs<DT> nxt;
-    int row = blockIdx.x * kWaves + wv;
-    if (row < M && lane < nchunks) load_regs<DT>(x, (size_t)row * K + (size_t)lane * kChunk, nxt);
+    // One chunk buffer, loaded one pass ahead: while pass p is rotated, the
+    // wave already loads its next live pass of the row, or its first pass of
+    // the workgroup's next row.  Loads are unconditional (a lane past the row
+    // end reads the pass's first chunk, the last row re-reads itself), so the
+    // load overwrites the buffer it was just converted from without a merge of
+    // old and new values.
+    ChunkRegs<DT> buf;
+    int row = blockIdx.x;     // < M: the grid never exceeds M
+    {
+        const int c0 = wv * 64;   // < nchunks: W <= number of passes of a row
+        load_regs<DT>(x, (size_t)row * K + (size_t)(c0 + lane < nchunks ? c0 + lane : c0) * kChunk, buf);
+    }
 
-    for (; row < M; row += nwaves) {
-        Held<DT> hv[NPMAX];
+    for (int it = 0; row < M; row += gridDim.x, ++it) {
+        const int nrow = row + gridDim.x < M ? row + gridDim.x : row;
+        Held<DT> hv[P];
         float lmax = 0.0f;
 #pragma unroll
-        for (int p = 0; p < NPMAX; ++p) {
-            if (p < np) {
-                ChunkRegs<DT> cur = nxt;
-                {   // prefetch: next pass of this row, or the first pass of the next row
-                    const int nr = (p + 1 < np) ? row : row + nwaves;
-                    const int nc = (p + 1 < np) ? (p + 1) * 64 + lane : lane;
-                    if (nr < M && nc < nchunks) load_regs<DT>(x, (size_t)nr * K + (size_t)nc * kChunk, nxt);
-                }
-                const int c = p * 64 + lane;
+        for (int p = 0; p < P; ++p) {
+            const int c0 = (p * W + wv) * 64;     // wave-uniform
+            if (c0 < nchunks) {
+                const int c = c0 + lane;
                 const bool ok = c < nchunks;
+                if ((nchunks & 63) && !ok) buf = ChunkRegs<DT>{};   // ragged last pass: zeros
                 double v[16];
-                if (nchunks & 63) {             // ragged last pass (wave-uniform branch)
-                    if (!ok) cur = ChunkRegs<DT>{};
+                regs_to_f64<DT>(buf, v);
+                {   // prefetch
+                    const int n0 = ((p + 1) * W + wv) * 64;
+                    const bool same = p + 1 < P && n0 < nchunks;
+                    const int lr = same ? row : nrow;
+                    const int l0 = same ? n0 : wv * 64;
+                    load_regs<DT>(x, (size_t)lr * K + (size_t)(l0 + lane < nchunks ? l0 + lane : l0) * kChunk, buf);
                 }
-                regs_to_f64<DT>(cur, v);
-                if constexpr (G == 16) {
-                    stage16<1>(v, 1.0);
-                    stage16<4>(v, 0.25);
-                } else {
-                    stage16<1>(v, 1.0);
-                    stage16<4>(v, 1.0);
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) tbuf[lane * kPad + i] = v[i];
-                    wave_sync();
-                    if constexpr (G == 256) {
-#pragma unroll
-                        for (int m = 0; m < 16; ++m) v[m] = tbuf[(gfirst + m) * kPad + gl];
-                        stage16<1>(v, 1.0);
-                        stage16<4>(v, 1.0 / 16.0);
-                    } else {
-#pragma unroll
-                        for (int b = 0; b < 4; ++b)
-#pragma unroll
-                            for (int a = 0; a < 4; ++a) v[a + 4 * b] = tbuf[(gfirst + b) * kPad + 4 * gl + a];
-                        stage16<4>(v, 1.0 / 8.0);
-                    }
-                    wave_sync();
-                }
-#pragma unroll
-                for (int i = 0; i < 16; i += 2) {
-                    if constexpr (DT == DT_BF16) {
-                        const float f0 = jam_to_f32(v[i]), f1 = jam_to_f32(v[i + 1]);
-                        hv[p].w[i >> 1] = pack_bf16x2(f0, f1);
-                        lmax = fmaxf(lmax, fmaxf(fabsf(f0), fabsf(f1)));
-                    } else {
-                        const float r0 = round_f64_to_dt<DT>(v[i]);
-                        const float r1 = round_f64_to_dt<DT>(v[i + 1]);
-                        hold<DT>(hv[p], i, r0, r1);
-                        lmax = fmaxf(lmax, fmaxf(fabsf(r0), fabsf(r1)));
-                    }
-                }
+                rotate_chunk<G>(v, tbuf, lane, gl, gfirst);
+                hold_chunk<DT>(v, hv[p], lmax);
             }
         }
-        // row absmax across the wave (invalid chunks hold zeros)
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, off));
-        // bf16: lmax is a jammed value; its RNE is the max of the rounded values
+        // row absmax: across the wave (lmax is never NaN: it starts at 0 and
+        // v_max3 drops NaN operands), then across the W waves
+        lmax = wave_max_nonneg(lmax);
+        if (W > 1) {
+            float* rb = red + (it & 1) * 8;
+            if (lane == 0) rb[wv] = lmax;
+            __syncthreads();
+            const float4 r0 = reinterpret_cast<const float4*>(rb)[0];
+            const float4 r1 = reinterpret_cast<const float4*>(rb)[1];
+            lmax = fmax3(fmax3(r0.x, r0.y, r0.z), fmax3(r0.w, r1.x, r1.y), fmax3(r1.z, r1.w, 0.0f));
+        }
         const float a = fmaxf(round_to_dt<DT>(lmax), clamp_floor<DT>());
-        const float s = round_to_dt<DT>(a / QMAX);
-        if (lane == 0) sout[row] = s;
-        const float rinv32 = 1.0f / s;
+        // s = RNE_DT(fl32(a / QMAX)).  a is a DT value of p <= 11 significant
+        // bits and QMAX is odd, so a / QMAX is never a DT rounding midpoint and
+        // lies at least 2^(-p-1) / QMAX >= 2^-19 (relative) from every one (a
+        // midpoint is an odd multiple of a half unit; a * 2^k / QMAX with a
+        // multiple of 2 above it is not); fl32(a / QMAX) and a * fl32(1 / QMAX),
+        // both within 2^-23 of a / QMAX, round to the same DT value.
+        const float s = DT == DT_F32 ? a / QMAX : round_to_dt<DT>(a * (1.0f / QMAX));
+        if (wv == 0 && lane == 0) sout[row] = s;
+        // bf16: v_rcp_f32 is within 1 ulp of 1 / s, so xr * rinv32 stays within
+        // 2^-22 of xr / s, inside the 2^-17 the quotient keeps from every bf16
+        // midpoint (file header)
+        const float rinv32 = __builtin_amdgcn_rcpf(s);
         const double rinv = 1.0 / (double)s;
 
 #pragma unroll
-        for (int p = 0; p < NPMAX; ++p) {
-            if (p < np) {
-                const int c = p * 64 + lane;
-                const bool ok = c < nchunks;
+        for (int p = 0; p < P; ++p) {
+            const int c0 = (p * W + wv) * 64;
+            if (c0 >= nchunks) continue;
+            const int c = c0 + lane;
+            const bool ok = c < nchunks;
 #pragma unroll
-                for (int i = 0; i < 16; i += 2) {
-                    float z0, z1;
-                    if constexpr (DT == DT_BF16) {
-                        // one packed RNE for both quotients; |z| <= QMAX (1 + 2^-9) because
-                        // s = RNE(absmax / QMAX), so rint stays in [-QMAX, QMAX]; the int8
-                        // clamp only guards non-finite input
-                        const uint32_t zz = pack_bf16x2(bf16lo_to_f32(hv[p].w[i >> 1]) * rinv32,
-                                                        bf16hi_to_f32(hv[p].w[i >> 1]) * rinv32);
-                        z0 = bf16lo_to_f32(zz);
-                        z1 = bf16hi_to_f32(zz);
-                        if constexpr (INT8) {
-                            z0 = fminf(fmaxf(z0, -QMAX), QMAX);
-                            z1 = fminf(fmaxf(z1, -QMAX), QMAX);
-                        }
-                    } else {
-                        float zz[2];
-#pragma unroll
-                        for (int h = 0; h < 2; ++h) {
-                            const float xv = held<DT>(hv[p], i + h);
-                            float z;
-                            if constexpr (DT == DT_F32) z = xv / s;
-                            else z = round_to_dt<DT>((float)((double)xv * rinv));
-                            if constexpr (DT == DT_F16) z = (z == z) ? z : 0.0f;
-                            zz[h] = fminf(fmaxf(z, -QMAX), QMAX);
-                        }
-                        z0 = zz[0];
-                        z1 = zz[1];
-                    }
-                    const int e0 = final_elem<G>(gl, i), e1 = final_elem<G>(gl, i + 1);
-                    if constexpr (B6) {
-                        // rint_even(z) as a float (+0 for zero), kept as its bf16 bits (exact:
-                        // an integer of magnitude <= 7)
-                        const float q0 = (z0 + kMagic) - kMagic, q1 = (z1 + kMagic) - kMagic;
-                        *b6_slot(gfirst + e0 / kChunk, e0 % kChunk) = (uint16_t)(__float_as_uint(q0) >> 16);
-                        *b6_slot(gfirst + e1 / kChunk, e1 % kChunk) = (uint16_t)(__float_as_uint(q1) >> 16);
-                    } else {
-                        // low byte of the float bits of z + 1.5*2^23 is rint_even(z) (two's complement)
-                        cb[(gfirst + e0 / kChunk) * 16 + (e0 % kChunk)] = (uint8_t)__float_as_uint(z0 + kMagic);
-                        cb[(gfirst + e1 / kChunk) * 16 + (e1 % kChunk)] = (uint8_t)__float_as_uint(z1 + kMagic);
-                    }
-                }
-                wave_sync();
-                uint4 w = {}, gq[4];        // gq: filled and used on even lanes only (B6T)
-                if constexpr (B6) {
-                    // the even lane of a pair reads the pair's 32 codes (64 bytes)
-                    if ((lane & 1) == 0) {
-#pragma unroll
-                        for (int h = 0; h < 4; ++h) gq[h] = reinterpret_cast<const uint4*>(b6_slot(lane, 0))[h];
+            for (int i = 0; i < 16; i += 2) {
+                float z0, z1;
+                if constexpr (DT == DT_BF16) {
+                    // one packed RNE for both quotients; |z| <= QMAX (1 + 2^-9) because
+                    // s = RNE(absmax / QMAX), so rint stays in [-QMAX, QMAX]; the int8
+                    // clamp only guards non-finite input
+                    const uint32_t zz = pack_bf16x2(bf16lo_to_f32(hv[p].w[i >> 1]) * rinv32,
+                                                    bf16hi_to_f32(hv[p].w[i >> 1]) * rinv32);
+                    z0 = bf16lo_to_f32(zz);
+                    z1 = bf16hi_to_f32(zz);
+                    if constexpr (INT8) {
+                        z0 = fminf(fmaxf(z0, -QMAX), QMAX);
+                        z1 = fminf(fmaxf(z1, -QMAX), QMAX);
                     }
                 } else {
-                    w = reinterpret_cast<const uint4*>(cb)[lane];
-                }
-                wave_sync();
-                if (OUT == OUT_I8 && ok) {
-                    *reinterpret_cast<uint4*>(qout + (size_t)row * K + (size_t)c * kChunk) = w;
-                } else if (OUT == OUT_I8T && ok) {
-                    const int k0 = c * kChunk;
-                    int8_t* chunk = qout + ((size_t)(row >> 8) * (K >> 6) + (k0 >> 6)) * I8T_CHUNK;
-                    *reinterpret_cast<uint4*>(chunk + i8t_off(row & 255, (k0 >> 4) & 3)) = w;
-                } else if (B6 && ok) {
-                    // chunks (2g', 2g'+1) are the 32 codes of one MFMA group: the even lane
-                    // converts them (bf16 values, element order) with the 32-wide BF6
-                    // converter and stores the group's 6 dwords
-                    if ((lane & 1) == 0) {
-                        const v16u words = {gq[0].x, gq[0].y, gq[0].z, gq[0].w, gq[1].x, gq[1].y, gq[1].z, gq[1].w,
-                                            gq[2].x, gq[2].y, gq[2].z, gq[2].w, gq[3].x, gq[3].y, gq[3].z, gq[3].w};
-                        const v6u r = __builtin_amdgcn_cvt_scalef32_pk32_bf6_bf16(__builtin_bit_cast(v32bf, words), 1.0f);
-                        const uint32_t d[6] = {r[0], r[1], r[2], r[3], r[4], r[5]};
-                        b6_store_group(qout, row, K, c * kChunk, d);
-                    }
-                } else if (ok) {
-                    const uint32_t ws[4] = {w.x & 0x0f0f0f0fu, w.y & 0x0f0f0f0fu, w.z & 0x0f0f0f0fu,
-                                            w.w & 0x0f0f0f0fu};
-                    uint32_t o[2];
+                    float zz[2];
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
-                        const uint32_t t0 = ws[2 * h] | (ws[2 * h] >> 4);
-                        const uint32_t t1 = ws[2 * h + 1] | (ws[2 * h + 1] >> 4);
-                        o[h] = (t0 & 0xffu) | ((t0 >> 8) & 0xff00u) | ((t1 & 0xffu) << 16) | ((t1 << 8) & 0xff000000u);
+                        const float xv = held<DT>(hv[p], i + h);
+                        float z;
+                        if constexpr (DT == DT_F32) z = xv / s;
+                        else z = round_to_dt<DT>((float)((double)xv * rinv));
+                        if constexpr (DT == DT_F16) z = (z == z) ? z : 0.0f;
+                        zz[h] = fminf(fmaxf(z, -QMAX), QMAX);
                     }
-                    *reinterpret_cast<uint2*>(qout + (size_t)row * (K / 2) + (size_t)c * (kChunk / 2)) =
-                        make_uint2(o[0], o[1]);
+                    z0 = zz[0];
+                    z1 = zz[1];
                 }
+                const int e0 = final_elem<G>(gl, i), e1 = final_elem<G>(gl, i + 1);
+                if constexpr (B6) {
+                    // rint_even(z) as a float, kept as its bf16 bits (exact: an integer of
+                    // magnitude <= 7; a zero code may carry the sign of z)
+                    const float q0 = __builtin_rintf(z0), q1 = __builtin_rintf(z1);
+                    *b6_slot(gfirst + e0 / kChunk, e0 % kChunk) = (uint16_t)(__float_as_uint(q0) >> 16);
+                    *b6_slot(gfirst + e1 / kChunk, e1 % kChunk) = (uint16_t)(__float_as_uint(q1) >> 16);
+                } else {
+                    // low byte of the float bits of z + 1.5*2^23 is rint_even(z) (two's complement)
+                    cb[(gfirst + e0 / kChunk) * 16 + (e0 % kChunk)] = (uint8_t)__float_as_uint(z0 + kMagic);
+                    cb[(gfirst + e1 / kChunk) * 16 + (e1 % kChunk)] = (uint8_t)__float_as_uint(z1 + kMagic);
+                }
+            }
+            wave_sync();
+            uint4 w = {}, gq[4];        // gq: filled and used on even lanes only (B6T)
+            if constexpr (B6) {
+                // the even lane of a pair reads the pair's 32 codes (64 bytes)
+                if ((lane & 1) == 0) {
+#pragma unroll
+                    for (int h = 0; h < 4; ++h) gq[h] = reinterpret_cast<const uint4*>(b6_slot(lane, 0))[h];
+                }
+            } else {
+                w = reinterpret_cast<const uint4*>(cb)[lane];
+            }
+            wave_sync();
+            if (OUT == OUT_I8 && ok) {
+                *reinterpret_cast<uint4*>(qout + (size_t)row * K + (size_t)c * kChunk) = w;
+            } else if (OUT == OUT_I8T && ok) {
+                const int k0 = c * kChunk;
+                int8_t* chunk = qout + ((size_t)(row >> 8) * (K >> 6) + (k0 >> 6)) * I8T_CHUNK;
+                *reinterpret_cast<uint4*>(chunk + i8t_off(row & 255, (k0 >> 4) & 3)) = w;
+            } else if (B6 && ok) {
+                // chunks (2g', 2g'+1) are the 32 codes of one MFMA group: the even lane
+                // converts them (bf16 values, element order) with the 32-wide BF6
+                // converter and stores the group's 6 dwords
+                if ((lane & 1) == 0) {
+                    const v16u words = {gq[0].x, gq[0].y, gq[0].z, gq[0].w, gq[1].x, gq[1].y, gq[1].z, gq[1].w,
+                                        gq[2].x, gq[2].y, gq[2].z, gq[2].w, gq[3].x, gq[3].y, gq[3].z, gq[3].w};
+                    const v6u r = __builtin_amdgcn_cvt_scalef32_pk32_bf6_bf16(__builtin_bit_cast(v32bf, words), 1.0f);
+                    const uint32_t d[6] = {r[0], r[1], r[2], r[3], r[4], r[5]};
+                    b6_store_group(qout, row, K, c * kChunk, d);
+                }
+            } else if (ok) {
+                const uint32_t ws[4] = {w.x & 0x0f0f0f0fu, w.y & 0x0f0f0f0fu, w.z & 0x0f0f0f0fu,
+                                        w.w & 0x0f0f0f0fu};
+                uint32_t o[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t t0 = ws[2 * h] | (ws[2 * h] >> 4);
+                    const uint32_t t1 = ws[2 * h + 1] | (ws[2 * h + 1] >> 4);
+                    o[h] = (t0 & 0xffu) | ((t0 >> 8) & 0xff00u) | ((t1 & 0xffu) << 16) | ((t1 << 8) & 0xff000000u);
+                }
+                *reinterpret_cast<uint2*>(qout + (size_t)row * (K / 2) + (size_t)c * (kChunk / 2)) =
+                    make_uint2(o[0], o[1]);
             }
         }
     }
     if constexpr (OUT == OUT_I8T) {   // zero codes in the padding rows of the last 256-row tile
         const int mpad = (M + 255) & ~255;
-        for (int prow = M + blockIdx.x * kWaves + wv; prow < mpad; prow += nwaves)
-            for (int k0 = 16 * lane; k0 < K; k0 += 16 * 64) {
+        for (int prow = M + blockIdx.x; prow < mpad; prow += gridDim.x)
+            for (int k0 = 16 * (wv * 64 + lane); k0 < K; k0 += 16 * 64 * W) {
                 int8_t* chunk = qout + ((size_t)(prow >> 8) * (K >> 6) + (k0 >> 6)) * I8T_CHUNK;
                 *reinterpret_cast<uint4*>(chunk + i8t_off(prow & 255, (k0 >> 4) & 3)) = make_uint4(0u, 0u, 0u, 0u);
             }
@@ -599,8 +682,8 @@ __global__ __launch_bounds__(64 * kWaves) void rotquant_wave_kernel(
     if constexpr (B6) {   // zero codes in the padding rows of the last 256-row tile
         const int mpad = (M + 255) & ~255;
         const uint32_t z[6] = {0u, 0u, 0u, 0u, 0u, 0u};
-        for (int prow = M + blockIdx.x * kWaves + wv; prow < mpad; prow += nwaves)
-            for (int k0 = 32 * lane; k0 < K; k0 += 32 * 64) b6_store_group(qout, prow, K, k0, z);
+        for (int prow = M + blockIdx.x; prow < mpad; prow += gridDim.x)
+            for (int k0 = 32 * (wv * 64 + lane); k0 < K; k0 += 32 * 64 * W) b6_store_group(qout, prow, K, k0, z);
     }
 }
 
@@ -618,25 +701,41 @@ static int num_cus() {
     return g_num_cus;
 }
 
+// Launch shape: a row is np = ceil(K / 1024) passes of 64 lanes; W <= 4 waves
+// of a workgroup share it with P = ceil(np / W) passes each: one pass per wave
+// up to np = 4, else 2 or 3 (K = 3072: 3 waves x 1 pass, measured 16.1 us at
+// M = 4608 against 17.5 for 1 wave x 3 passes; K = 12288: 4 waves x 3 passes,
+// 51.3 us against 53.7 for 3 x 4 and 63.9 for 6 x 2).  The grid is the number
+// of workgroups that fit on the chip at once, lowered so that every workgroup
+// walks the same number of rows.
 template <int DT, int G, int OUT>
-static hipError_t rq_wave_launch(const void* x, int8_t* q, float* s, int M, int K, hipStream_t st) {
+static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K, hipStream_t st) {
+    if (M <= 0) return hipSuccess;
     const int np = (K / kChunk + 63) / 64;
-    // enough waves to keep every CU busy; each wave then walks rows persistently
-    const int max_wg = num_cus() * 8;
-    int grid = (M + kWaves - 1) / kWaves;
-    if (grid > max_wg) grid = max_wg;
-    if (grid < 1) grid = 1;
-    dim3 g(grid), b(64 * kWaves);
-    if (np <= 3)
-        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 3, OUT>), g, b, 0, st, x, q, s, M, K);
-    else if (np <= 6)
-        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 6, OUT>), g, b, 0, st, x, q, s, M, K);
-    else
-        hipLaunchKernelGGL((rotquant_wave_kernel<DT, G, 12, OUT>), g, b, 0, st, x, q, s, M, K);
+    int P = np <= kRowMaxWaves ? 1 : np <= 2 * kRowMaxWaves && np % 3 != 0 ? 2 : 3;
+    int W = (np + P - 1) / P;
+    P = (np + W - 1) / W;
+    if (W > kRowMaxWaves || P > kRowMaxPass) return hipErrorInvalidValue;
+    const size_t lds = (size_t)W * kRowWaveLds + 16 * sizeof(float);
+    void (*kern)(const void*, int8_t*, float*, int, int) =
+        P == 1 ? rotquant_row_kernel<DT, G, 1, OUT> : P == 2 ? rotquant_row_kernel<DT, G, 2, OUT>
+                                                             : rotquant_row_kernel<DT, G, 3, OUT>;
+    static int occupancy[kRowMaxPass + 1][kRowMaxWaves + 1];   // workgroups per CU, per shape
+    int per_cu = occupancy[P][W];
+    if (per_cu == 0) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64 * W, lds) != hipSuccess || per_cu < 1)
+            per_cu = 1;
+        occupancy[P][W] = per_cu;
+    }
+    int grid = num_cus() * per_cu;
+    if (grid > M) grid = M;
+    const int rows = (M + grid - 1) / grid;
+    grid = (M + rows - 1) / rows;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * W), lds, st, x, q, s, M, K);
     return hipGetLastError();
 }
 
-constexpr int kWaveMaxK = 12 * 64 * kChunk;   // 12288
+constexpr int kWaveMaxK = kRowMaxWaves * kRowMaxPass * 64 * kChunk;   // 12288
 
 // ---------------------------------------------------------------------------
 // host-side launch
@@ -665,7 +764,7 @@ template <int DT, int G, bool STOCH, bool I8 = false>
 static hipError_t rq_launch_g(const void* x, const void* noise, int8_t* q, float* s, int M, int K,
                               hipStream_t st) {
     if (M == 0) return hipSuccess;
-    if (!STOCH && K <= kWaveMaxK) return rq_wave_launch<DT, G, I8 ? OUT_I8 : OUT_PACK4>(x, q, s, M, K, st);
+    if (!STOCH && K <= kWaveMaxK) return rq_row_launch<DT, G, I8 ? OUT_I8 : OUT_PACK4>(x, q, s, M, K, st);
     RQPlan pl;
     if (rq_plan(M, K, G, &pl) != 0) return hipErrorInvalidValue;
     dim3 grid(pl.grid), block(pl.block);
@@ -716,9 +815,9 @@ hipError_t rotquant_b6_launch(const void* x, int in_dtype, uint8_t* a6, float* s
     int8_t* q = reinterpret_cast<int8_t*>(a6);
 #define RB6_G(DT)                                                                                   \
     switch (G) {                                                                                    \
-        case 16: return rq_wave_launch<DT, 16, OUT_B6T>(x, q, s, M, K, st);                         \
-        case 64: return rq_wave_launch<DT, 64, OUT_B6T>(x, q, s, M, K, st);                         \
-        case 256: return rq_wave_launch<DT, 256, OUT_B6T>(x, q, s, M, K, st);                       \
+        case 16: return rq_row_launch<DT, 16, OUT_B6T>(x, q, s, M, K, st);                         \
+        case 64: return rq_row_launch<DT, 64, OUT_B6T>(x, q, s, M, K, st);                         \
+        case 256: return rq_row_launch<DT, 256, OUT_B6T>(x, q, s, M, K, st);                       \
         default: return hipErrorInvalidValue;                                                       \
     }
     switch (in_dtype) {
@@ -738,9 +837,9 @@ hipError_t rotquant_i8t_launch(const void* x, int in_dtype, int8_t* q, float* s,
     if (K % 64 != 0 || K > kWaveMaxK || M < 0) return hipErrorInvalidValue;
 #define RI8T_G(DT)                                                                                  \
     switch (G) {                                                                                    \
-        case 16: return rq_wave_launch<DT, 16, OUT_I8T>(x, q, s, M, K, st);                         \
-        case 64: return rq_wave_launch<DT, 64, OUT_I8T>(x, q, s, M, K, st);                         \
-        case 256: return rq_wave_launch<DT, 256, OUT_I8T>(x, q, s, M, K, st);                       \
+        case 16: return rq_row_launch<DT, 16, OUT_I8T>(x, q, s, M, K, st);                         \
+        case 64: return rq_row_launch<DT, 64, OUT_I8T>(x, q, s, M, K, st);                         \
+        case 256: return rq_row_launch<DT, 256, OUT_I8T>(x, q, s, M, K, st);                       \
         default: return hipErrorInvalidValue;                                                       \
     }
     switch (in_dtype) {
