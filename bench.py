@@ -268,9 +268,9 @@ def main():
             "traffic": gemm_traffic_bytes() if args.path == "bf6" else None,
         },
         "rotate_quant": {
-            "kernel": {"bf6": "rotquant_wave_kernel<bf16,256,3,B6T out>",
-                       "int8": "rotquant_wave_kernel<bf16,256,3,packed int4 out>",
-                       "w8a8": "rotquant_wave_kernel<bf16,256,3,I8T out>"}[args.path],
+            "kernel": {"bf6": "rotquant_row_kernel<bf16,256,1 pass,B6T out> (3 waves per row)",
+                       "int8": "rotquant_row_kernel<bf16,256,1 pass,packed int4 out> (3 waves per row)",
+                       "w8a8": "rotquant_row_kernel<bf16,256,1 pass,I8T out> (3 waves per row)"}[args.path],
             "bound": "hbm",
             "GBps_at_M4608_K3072": round(metric_rq_gbs, 1),
             "frac_at_M4608_K3072": round(metric_rq_gbs / PEAK_HBM_GBS, 4),
