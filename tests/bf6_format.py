@@ -1,4 +1,4 @@
-"""numpy decoder of the B6T operand layout of the bf6 GEMM path (test helper).
+"""numpy helpers for the operand layouts of the GEMM paths (test helper): the B6T decoder of the bf6 path and the I8T re-layout of the W8A8 path.
 
 B6T of a [rows, K] matrix (K % 128 == 0): rows padded to R = ceil(rows/256)*256
 (zero codes), stored as [R/256][K/128] chunks of 24576 bytes.  Group g of row r
@@ -64,3 +64,19 @@ def unpack_int4(packed: np.ndarray) -> np.ndarray:
     lo = ((p & 15) ^ 8) - 8
     hi = ((p >> 4) ^ 8) - 8
     return np.stack([lo, hi], -1).reshape(packed.shape[0], -1)
+
+
+def i8t_np(q):
+    """Host re-layout of int8 codes [rows, K] into I8T, written from the layout's
+    definition: [ceil(rows/256)][K/64] chunks of 256 rows x 64 bytes, row r at
+    r*64, its 16-byte piece c at (c ^ f(r))*16, padding rows zero."""
+    rows, K = q.shape
+    tiles, nkb = (rows + 255) // 256, K // 64
+    qp = np.zeros((tiles * 256, K), dtype=np.int8)
+    qp[:rows] = q
+    qt = qp.reshape(tiles, 256, nkb, 4, 16).transpose(0, 2, 1, 3, 4)        # [t, kb, r, c, 16]
+    r = np.arange(256)
+    f = (((r >> 1) ^ (r >> 3)) & 1) | ((r >> 1) & 2)
+    idx = np.arange(4)[None, :] ^ f[:, None]                                  # slot p holds piece p ^ f(r)
+    out = np.take_along_axis(qt, idx[None, None, :, :, None], axis=3)
+    return out.reshape(tiles * 256, K)

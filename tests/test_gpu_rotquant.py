@@ -118,3 +118,40 @@ def test_persistent_rows_sampled(native, oracle, gpu, M, K):
     eq, es, _ = oracle.rotquant(host_bits(x[rows]), 1, 256)
     assert np.array_equal(q.cpu().numpy()[rows], eq)
     assert np.array_equal(s.cpu().numpy()[rows], es)
+
+
+# Every launch shape of the row-split kernel: W waves per row x P passes per
+# wave (K = 1024 .. 11264 gives 1x1, 2x1, 4x1, 3x2, 2x3, 4x2, 3x3, 4x3), rows
+# whose last wave or last pass starts past the row end (5120, 7168, 10240,
+# 11264), lanes past the row end (640, 1152, 2176), and workgroups walking
+# several rows (M above the resident grid).
+ROW_SPLIT_SHAPES = [(300, 1024, 256), (1500, 2048, 256), (700, 4096, 256), (3000, 5120, 256),
+                    (90, 6144, 256), (1300, 7168, 256), (64, 8192, 256), (2100, 9216, 256),
+                    (33, 10240, 256), (1700, 11264, 256), (500, 640, 64), (2600, 1152, 64), (77, 2176, 64)]
+
+
+@pytest.mark.parametrize("M,K,G", ROW_SPLIT_SHAPES)
+def test_row_split_launch_shapes(native, oracle, gpu, M, K, G):
+    """Packed int4 and int8 codes against the oracle (sampled rows); the B6T and
+    I8T layouts against those codes (all rows)."""
+    print(f"row-split M={M} K={K} G={G}", flush=True)
+    from bf6_format import decode_b6t, i8t_np, unpack_int4
+    x = outlier_activations(M, K, seed=M + 7 * K)
+    xg = x.cuda()
+    q, s = native.convrot_quant_int4(xg, G)
+    a6, s6 = native.convrot_quant_bf6(xg, G)
+    q8, s8 = native.convrot_quant_int8(xg, G)
+    q8t, s8t = native.convrot_quant_int8_i8t(xg, G)
+    torch.cuda.synchronize()
+    rows = np.arange(M) if M <= 128 else np.concatenate(
+        [np.random.RandomState(K).choice(M, 48, replace=False), [0, 1, M - 2, M - 1]])
+    eq, es, _ = oracle.rotquant(host_bits(x[rows]), 1, G)
+    assert np.array_equal(q.cpu().numpy()[rows], eq)
+    assert np.array_equal(s.cpu().numpy()[rows], es)
+    eq8, es8, _ = oracle.rotquant8(host_bits(x[rows]), 1, G)
+    assert np.array_equal(q8.cpu().numpy()[rows], eq8)
+    assert np.array_equal(s8.cpu().numpy()[rows], es8)
+    assert torch.equal(s6.view(torch.int32), s.view(torch.int32))
+    assert torch.equal(s8t.view(torch.int32), s8.view(torch.int32))
+    assert np.array_equal(decode_b6t(a6.cpu().numpy(), M), unpack_int4(q.cpu().numpy()))
+    assert np.array_equal(q8t.cpu().numpy(), i8t_np(q8.cpu().numpy()))

@@ -9,6 +9,7 @@ import numpy as np
 import pytest
 import torch
 
+from bf6_format import i8t_np
 from inputs import (bf16_bits, clamp_rows8, config1_weight, edge_cases, normal_bias, normal_weight,
                     outlier_activations, small_w8a8_case)
 
@@ -178,22 +179,6 @@ def _ops():
 # I8T: the tile-major int8 operand layout of the W8A8 GEMM (the linear's path
 # when K % 64 == 0)
 # ---------------------------------------------------------------------------
-
-def i8t_np(q):
-    """Host re-layout of int8 codes [rows, K] into I8T, written from the layout's
-    definition: [ceil(rows/256)][K/64] chunks of 256 rows x 64 bytes, row r at
-    r*64, its 16-byte piece c at (c ^ f(r))*16, padding rows zero."""
-    rows, K = q.shape
-    tiles, nkb = (rows + 255) // 256, K // 64
-    qp = np.zeros((tiles * 256, K), dtype=np.int8)
-    qp[:rows] = q
-    qt = qp.reshape(tiles, 256, nkb, 4, 16).transpose(0, 2, 1, 3, 4)        # [t, kb, r, c, 16]
-    r = np.arange(256)
-    f = (((r >> 1) ^ (r >> 3)) & 1) | ((r >> 1) & 2)
-    idx = np.arange(4)[None, :] ^ f[:, None]                                  # slot p holds piece p ^ f(r)
-    out = np.take_along_axis(qt, idx[None, None, :, :, None], axis=3)
-    return out.reshape(tiles * 256, K)
-
 
 I8T_QUANT_CASES = [(1, 256, 256, torch.bfloat16), (33, 192, 64, torch.bfloat16), (300, 3072, 256, torch.bfloat16),
                    (257, 12288, 256, torch.bfloat16), (65, 3072, 256, torch.float16), (17, 512, 64, torch.float32),
