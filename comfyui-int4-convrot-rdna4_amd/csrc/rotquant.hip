@@ -288,7 +288,7 @@ __global__ __launch_bounds__(kMaxThreads) void rotquant_kernel(
 // ---------------------------------------------------------------------------
 
 constexpr int kRowMaxWaves = 4;                        // waves per workgroup
-constexpr int kRowMaxPass = 3;                         // passes per wave
+constexpr int kRowMaxPass = 6;                         // passes per wave
 constexpr int kRowWaveLds = 64 * kPad * 8;             // LDS bytes per wave
 
 typedef unsigned v16u __attribute__((ext_vector_type(16)));
@@ -703,23 +703,23 @@ static int num_cus() {
 
 // Launch shape: a row is np = ceil(K / 1024) passes of 64 lanes; W <= 4 waves
 // of a workgroup share it with P = ceil(np / W) passes each: one pass per wave
-// up to np = 4, else 2 or 3 (K = 3072: 3 waves x 1 pass, measured 16.1 us at
-// M = 4608 against 17.5 for 1 wave x 3 passes; K = 12288: 4 waves x 3 passes,
-// 51.3 us against 53.7 for 3 x 4 and 63.9 for 6 x 2).  The grid is the number
-// of workgroups that fit on the chip at once, lowered so that every workgroup
-// walks the same number of rows.
+// up to np = 4, 2 or 3 passes up to np = 8, else 2 waves of 5..6 passes.
+// Measured at M = 4608: K = 3072 3 waves x 1 pass 16.2 us (1 x 3: 17.7,
+// 2 x 2: 16.7); K = 12288 2 x 6 48.9 us (4 x 3: 52.1, 3 x 4: 54.9, 6 x 2:
+// 65.2, 12 x 1: 54.7).  The grid is the number of workgroups that fit on the
+// chip at once, lowered so that every workgroup walks the same number of rows.
 template <int DT, int G, int OUT>
 static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K, hipStream_t st) {
     if (M <= 0) return hipSuccess;
     const int np = (K / kChunk + 63) / 64;
-    int P = np <= kRowMaxWaves ? 1 : np <= 2 * kRowMaxWaves && np % 3 != 0 ? 2 : 3;
+    int P = np <= kRowMaxWaves ? 1 : np <= 2 * kRowMaxWaves ? (np % 3 != 0 ? 2 : 3) : (np + 1) / 2;
     int W = (np + P - 1) / P;
     P = (np + W - 1) / W;
     if (W > kRowMaxWaves || P > kRowMaxPass) return hipErrorInvalidValue;
     const size_t lds = (size_t)W * kRowWaveLds + 16 * sizeof(float);
     void (*kern)(const void*, int8_t*, float*, int, int) =
         P == 1 ? rotquant_row_kernel<DT, G, 1, OUT> : P == 2 ? rotquant_row_kernel<DT, G, 2, OUT>
-                                                             : rotquant_row_kernel<DT, G, 3, OUT>;
+        : P == 3 ? rotquant_row_kernel<DT, G, 3, OUT> : rotquant_row_kernel<DT, G, 6, OUT>;   // 5..6 passes: 6
     static int occupancy[kRowMaxPass + 1][kRowMaxWaves + 1];   // workgroups per CU, per shape
     int per_cu = occupancy[P][W];
     if (per_cu == 0) {
@@ -735,7 +735,7 @@ static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K
     return hipGetLastError();
 }
 
-constexpr int kWaveMaxK = kRowMaxWaves * kRowMaxPass * 64 * kChunk;   // 12288
+constexpr int kWaveMaxK = 12 * 64 * kChunk;   // 12288: 2 waves x 6 passes
 
 // ---------------------------------------------------------------------------
 // host-side launch
