@@ -236,11 +236,6 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
         }
     }
     const uint32_t lds_base = (uint32_t)(uintptr_t)plds;
-    auto issue = [&](int kb) {
-        const uint32_t st = lds_base + (kb % P_STAGES) * P_STAGE_BYTES + wave * P_LOADS * 1024;
-#pragma unroll
-        for (int j = 0; j < P_LOADS; ++j) dma16(st + j * 1024, src[j] + kb * P_ROWB);
-    };
 
     v16i acc[4][PFN];
 #pragma unroll
@@ -331,60 +326,97 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
         }
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));            // the copies past the end have landed
     } else {
-#pragma unroll
-    for (int p = 0; p < P_STAGES - 1; ++p)
-        if (p < nkb) issue(p);
-    for (int kb = 0; kb < nkb; ++kb) {
-        // block kb landed (blocks kb+1 .. min(kb+P_STAGES-2, nkb-1) may stay in flight)
-        wait_block_landed<P_STAGES - 2, P_LOADS>(min(P_STAGES - 2, nkb - 1 - kb));
-        __syncthreads();
-        if (kb + P_STAGES - 1 < nkb) issue(kb + P_STAGES - 1);
-        const uint8_t* la = plds + (kb % P_STAGES) * P_STAGE_BYTES;
-        const uint8_t* lb = la + P_BM * P_ROWB;
-        uint4 fa[2][4], fb[2][PFN];
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
+        // Packed int4: the W8A8 loop with the nibble unpack.  A 16-byte fragment (32
+        // nibbles of one row and k step) becomes two MFMA operands of 16 int8 values
+        // 16 q: its first 8 bytes the "lo" operand, its last 8 the "hi" one (both sides
+        // unpack alike, so the k order inside a step is immaterial; the epilogue drops
+        // the factor 256).  Two phases per 128-k block kb, one per k step of 64: the 8
+        // lo MFMAs, then the 8 hi ones.  In the 16 slots of a phase: the hi operands of
+        // this step are unpacked (slots 0..5, consumed from slot 8), the fragments of
+        // the next step are read (3..8), one DMA instruction goes out in slots 6 and 9
+        // (phase A: the second half of block kb+P_STAGES-2; phase B: the first half of
+        // block kb+P_STAGES-1), and the lo operands of the next step are unpacked
+        // (10..15, after this step's lo MFMAs).  Fragments are read and unpacked in
+        // the order the MFMAs consume them: B0, B1, A0..A3.
+        static_assert(P_LOADS == 4 && PFN == 2, "int4 schedule");
+        typedef unsigned v4u __attribute__((ext_vector_type(4)));
+        struct Frags { v4u fa[4], fb[2]; };
+        struct Ops { v4i alo[4], ahi[4], blo[2], bhi[2]; };
+        constexpr int kOrder[6] = {4, 5, 0, 1, 2, 3};    // fragment r: A row tile r < 4, else B tile r - 4
+        auto read_one = [&](int kb, int s2, int r, Frags& f) __attribute__((always_inline)) {
+            const uint8_t* la = plds + (kb % P_STAGES) * P_STAGE_BYTES;
             const int c = 2 * s2 + fhalf;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = wm * 128 + i * 32 + frow;
-                fa[s2][i] = *reinterpret_cast<const uint4*>(la + r * P_ROWB + swz(r, c) * 16);
+            if (r < 4) {
+                const int row = wm * 128 + r * 32 + frow;
+                f.fa[r] = *reinterpret_cast<const v4u*>(la + row * P_ROWB + swz(row, c) * 16);
+            } else {
+                const int row = wn * WTN_P + (r - 4) * 32 + frow;
+                f.fb[r - 4] = *reinterpret_cast<const v4u*>(la + P_BM * P_ROWB + row * P_ROWB + swz(row, c) * 16);
             }
+        };
+        // 8 packed bytes (16 nibbles) -> 16 int8 values 16 q (as unpack16)
+        auto unpack8 = [](unsigned x, unsigned y) __attribute__((always_inline)) {
+            return (v4i){(int)((x << 4) & 0xF0F0F0F0u), (int)(x & 0xF0F0F0F0u),
+                         (int)((y << 4) & 0xF0F0F0F0u), (int)(y & 0xF0F0F0F0u)};
+        };
+        auto unpack_lo = [&](const Frags& f, int r, Ops& o) __attribute__((always_inline)) {
+            if (r < 4) o.alo[r] = unpack8(f.fa[r].x, f.fa[r].y);
+            else o.blo[r - 4] = unpack8(f.fb[r - 4].x, f.fb[r - 4].y);
+        };
+        auto unpack_hi = [&](const Frags& f, int r, Ops& o) __attribute__((always_inline)) {
+            if (r < 4) o.ahi[r] = unpack8(f.fa[r].z, f.fa[r].w);
+            else o.bhi[r - 4] = unpack8(f.fb[r - 4].z, f.fb[r - 4].w);
+        };
+        // MFMA t (0..15) of a k step: lo operands for t < 8, hi for t >= 8; A tile (t & 7) / 2, B tile t % 2
+        auto mfma_one = [&](const Ops& o, int t) __attribute__((always_inline)) {
+            const int i = (t & 7) >> 1, j = t & 1;
+            if (t < 8) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.blo[j], o.alo[i], acc[i][j], 0, 0, 0);
+            else acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.bhi[j], o.ahi[i], acc[i][j], 0, 0, 0);
+        };
+        auto dma_one = [&](int kb, int j) __attribute__((always_inline)) {
+            const uint32_t st = lds_base + (kb % P_STAGES) * P_STAGE_BYTES + wave * P_LOADS * 1024;
+            dma16(st + j * 1024, src[j] + (size_t)min(kb, nkb - 1) * P_ROWB);
+        };
+        Frags F0, F1;
+        Ops O;
 #pragma unroll
-            for (int j = 0; j < PFN; ++j) {
-                const int r = wn * WTN_P + j * 32 + frow;
-                fb[s2][j] = *reinterpret_cast<const uint4*>(lb + r * P_ROWB + swz(r, c) * 16);
+        for (int p = 0; p < P_STAGES - 2; ++p)
+#pragma unroll
+            for (int j = 0; j < P_LOADS; ++j) dma_one(p, j);
+#pragma unroll
+        for (int j = 0; j < P_LOADS / 2; ++j) dma_one(P_STAGES - 2, j);   // the rest in phase A of block 0
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((P_STAGES - 3) * P_LOADS + P_LOADS / 2));   // block 0 landed
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < 6; ++r) read_one(0, 0, kOrder[r], F0);
+#pragma unroll
+        for (int r = 0; r < 6; ++r) unpack_lo(F0, kOrder[r], O);
+        for (int kb = 0; kb < nkb; ++kb) {
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {            // phase A: k step 0 of block kb
+                mfma_one(O, t);
+                __builtin_amdgcn_sched_barrier(0);
+                if (t < 6) unpack_hi(F0, kOrder[t], O);
+                if (t >= 3 && t < 9) read_one(kb, 1, kOrder[t - 3], F1);
+                if (t == 6 || t == 9) dma_one(kb + P_STAGES - 2, P_LOADS / 2 + (t == 6 ? 0 : 1));
+                if (t >= 10) unpack_lo(F1, kOrder[t - 10], O);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm((P_STAGES - 3) * P_LOADS));   // block kb+1 landed
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {            // phase B: k step 1 of block kb
+                mfma_one(O, t);
+                __builtin_amdgcn_sched_barrier(0);
+                if (t < 6) unpack_hi(F1, kOrder[t], O);
+                if (t >= 3 && t < 9) read_one(kb + 1, 0, kOrder[t - 3], F0);
+                if (t == 6 || t == 9) dma_one(kb + P_STAGES - 1, t == 6 ? 0 : 1);
+                if (t >= 10) unpack_lo(F0, kOrder[t - 10], O);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-#pragma unroll
-        for (int s2 = 0; s2 < 2 && I8; ++s2) {          // W8A8: the 16 bytes are the operand
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < PFN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i, fb[s2][j]),
-                                                                     __builtin_bit_cast(v4i, fa[s2][i]), acc[i][j],
-                                                                     0, 0, 0);
-        }
-#pragma unroll
-        for (int s2 = 0; s2 < 2 && !I8; ++s2) {
-            v4i a_lo[4], a_hi[4], b_lo[PFN], b_hi[PFN];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) unpack16(fa[s2][i], a_lo[i], a_hi[i]);
-#pragma unroll
-            for (int j = 0; j < PFN; ++j) unpack16(fb[s2][j], b_lo[j], b_hi[j]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < PFN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b_lo[j], a_lo[i], acc[i][j], 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < PFN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b_hi[j], a_hi[i], acc[i][j], 0, 0, 0);
-        }
-    }
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));            // the copies past the end have landed
     }
 
     __syncthreads();                                     // every wave is done with the stages
