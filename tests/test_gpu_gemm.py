@@ -23,8 +23,10 @@ def cu(a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
+# K = 128 / 384 run the pipelined kernel with one / three 128-k blocks (copies
+# past the last block clamped), K % 128 != 0 the register-staged one
 ACC_SHAPES = [(1, 1, 32), (3, 5, 64), (64, 48, 256), (256, 256, 3072), (300, 200, 160),
-              (257, 513, 1024), (512, 256, 12288), (100, 300, 3840), (16, 700, 96)]
+              (257, 513, 1024), (512, 256, 12288), (100, 300, 3840), (16, 700, 96), (9, 17, 128), (40, 260, 384)]
 
 
 @pytest.mark.parametrize("M,N,K", ACC_SHAPES)

@@ -76,7 +76,7 @@ def test_weight_int8_config1_golden(backend, goldens, gpu):
 
 
 ACC_SHAPES = [(1, 1, 16), (3, 5, 48), (64, 48, 256), (300, 200, 160), (257, 513, 1024), (100, 300, 3840),
-              (16, 700, 80), (512, 256, 12288), (31, 33, 4112)]
+              (16, 700, 80), (512, 256, 12288), (31, 33, 4112), (5, 9, 64), (12, 70, 128), (40, 33, 192)]
 
 
 @pytest.mark.parametrize("M,N,K", ACC_SHAPES)
@@ -196,7 +196,8 @@ def test_quant_int8_i8t_layout(native, gpu, M, K, G, dt):
     assert np.array_equal(native.int8_to_i8t(q).cpu().numpy(), want)
 
 
-I8T_GEMM_SHAPES = [(64, 48, 256), (257, 300, 3072), (33, 513, 1088), (512, 256, 64), (300, 700, 12288)]
+I8T_GEMM_SHAPES = [(64, 48, 256), (257, 300, 3072), (33, 513, 1088), (512, 256, 64), (300, 700, 12288),
+                   (20, 40, 128), (70, 90, 192)]   # one to three 64-k blocks
 
 
 @pytest.mark.parametrize("M,N,K", I8T_GEMM_SHAPES)
