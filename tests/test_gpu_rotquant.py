@@ -49,14 +49,14 @@ def test_shapes_bf16(native, oracle, gpu, M, K, G):
     assert_same(oracle, x, G, q, s)
 
 
-@pytest.mark.parametrize("M,K,G", [(19, 3072, 256), (8, 192, 64), (6, 80, 16), (130, 12288, 256)])
+@pytest.mark.parametrize("M,K,G", [(19, 3072, 256), (8, 192, 64), (6, 80, 16), (130, 12288, 256), (300, 9216, 256)])
 def test_shapes_f16(native, oracle, gpu, M, K, G):
     x = outlier_activations(M, K, seed=K + G, dtype=torch.float16, scale=8.0)
     q, s = gpu_quant(native, x, G)
     assert_same(oracle, x, G, q, s)
 
 
-@pytest.mark.parametrize("M,K,G", [(19, 3072, 256), (8, 192, 64), (6, 80, 16)])
+@pytest.mark.parametrize("M,K,G", [(19, 3072, 256), (8, 192, 64), (6, 80, 16), (40, 12288, 256), (600, 9216, 64)])
 def test_shapes_f32(native, oracle, gpu, M, K, G):
     # f32 values on a bf16 grid: every group sum is exact in fp64, so the
     # correctly rounded rotation is what both sides compute
