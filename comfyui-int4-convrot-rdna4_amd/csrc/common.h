@@ -6,10 +6,36 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace convrot {
 
 // dtype codes of the C-ABI (reference: _int4/hip_loader.py:38-39)
 enum : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
+
+// ---------------------------------------------------------------------------
+// host-side per-device set-up.  Launch helpers may be called from several
+// host threads at once, so their caches are atomics: concurrent first calls
+// on a device may each do the set-up, which is idempotent.
+// ---------------------------------------------------------------------------
+
+constexpr int kMaxDev = 64;
+
+// Index of the current device, checked against kMaxDev.
+inline hipError_t current_device(int* dev) {
+    hipError_t e = hipGetDevice(dev);
+    if (e != hipSuccess) return e;
+    return (*dev < 0 || *dev >= kMaxDev) ? hipErrorInvalidDevice : hipSuccess;
+}
+
+// Raises a kernel's dynamic-LDS limit to `bytes` on the current device, once.
+// A failed attempt leaves the flag clear, so the next call tries again.
+inline hipError_t lds_limit_once(std::atomic<bool> (&done)[kMaxDev], int dev, const void* kernel, int bytes) {
+    if (done[dev].load(std::memory_order_acquire)) return hipSuccess;
+    hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess) done[dev].store(true, std::memory_order_release);
+    return e;
+}
 
 __device__ __forceinline__ float bf16lo_to_f32(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16hi_to_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }

@@ -432,18 +432,13 @@ static hipError_t launch_epi(const int8_t* Xp, const int8_t* Wp, const float* xs
     if (TM || (I8 ? K : K / 2) % P_ROWB == 0) {
         constexpr int WN = CONVROT_PIPE_WN;
         const int ntiles = ((M + P_BM - 1) / P_BM) * ((N + P_BN - 1) / P_BN);
-        constexpr int kMaxDev = 64;
-        static bool attr_set[kMaxDev] = {};
+        static std::atomic<bool> attr_set[kMaxDev];
         int dev = 0;
-        hipError_t e = hipGetDevice(&dev);
+        hipError_t e = current_device(&dev);
         if (e != hipSuccess) return e;
-        if (dev < 0 || dev >= kMaxDev) return hipErrorInvalidDevice;
-        if (!attr_set[dev]) {
-            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_pipe_kernel<EPI, WN, LORA, I8, TM>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, P_LDS_BYTES);
-            if (e != hipSuccess) return e;
-            attr_set[dev] = true;
-        }
+        e = lds_limit_once(attr_set, dev,
+                           reinterpret_cast<const void*>(&w4a4_gemm_pipe_kernel<EPI, WN, LORA, I8, TM>), P_LDS_BYTES);
+        if (e != hipSuccess) return e;
         hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<EPI, WN, LORA, I8, TM>), dim3(ntiles), dim3(128 * WN),
                            P_LDS_BYTES, st, Xp, Wp, xs, ws, bias, out, M, N, K, la,
                            tile_group_rows((M + P_BM - 1) / P_BM));

@@ -350,33 +350,25 @@ template <int EPI, int LR>
 static hipError_t launch_bf6(const uint8_t* A6, const uint8_t* W6, const float* xs, const float* ws,
                              const void* bias, int bias_dt, void* out, int M, int N, int K, const LoraArgs& la,
                              int nsplit, float* part, hipStream_t st) {
-    constexpr int kMaxDev = 64;
-    static bool attr_set[kMaxDev] = {};
-    static bool attr_split[kMaxDev] = {};
+    static std::atomic<bool> attr_set[kMaxDev];
+    static std::atomic<bool> attr_split[kMaxDev];
     int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
+    hipError_t e = current_device(&dev);
     if (e != hipSuccess) return e;
-    if (dev < 0 || dev >= kMaxDev) return hipErrorInvalidDevice;
     const int tiles_m = (M + B6_BM - 1) / B6_BM;
     const int ntiles = tiles_m * ((N + B6_BN - 1) / B6_BN);
     if (nsplit <= 1) {
-        if (!attr_set[dev]) {
-            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_bf6_kernel<EPI, LR, false>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, B6_LDS_BYTES);
-            if (e != hipSuccess) return e;
-            attr_set[dev] = true;
-        }
+        e = lds_limit_once(attr_set, dev, reinterpret_cast<const void*>(&w4a4_gemm_bf6_kernel<EPI, LR, false>),
+                           B6_LDS_BYTES);
+        if (e != hipSuccess) return e;
         hipLaunchKernelGGL((w4a4_gemm_bf6_kernel<EPI, LR, false>), dim3(ntiles), dim3(B6_THREADS), B6_LDS_BYTES,
                            st, A6, W6, xs, ws, bias, bias_dt, out, M, N, K, la, tile_group_rows(tiles_m), 1, nullptr);
         return hipGetLastError();
     }
     // the partial kernel is the same for every epilogue and LoRA rank
-    if (!attr_split[dev]) {
-        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&w4a4_gemm_bf6_kernel<EPI_ACC, 0, true>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, B6_LDS_BYTES);
-        if (e != hipSuccess) return e;
-        attr_split[dev] = true;
-    }
+    e = lds_limit_once(attr_split, dev, reinterpret_cast<const void*>(&w4a4_gemm_bf6_kernel<EPI_ACC, 0, true>),
+                       B6_LDS_BYTES);
+    if (e != hipSuccess) return e;
     const LoraArgs none{nullptr, nullptr, 0, 0.0f};
     hipLaunchKernelGGL((w4a4_gemm_bf6_kernel<EPI_ACC, 0, true>), dim3(ntiles * nsplit), dim3(B6_THREADS),
                        B6_LDS_BYTES, st, A6, W6, nullptr, nullptr, nullptr, 0, nullptr, M, N, K, none, 1, nsplit, part);

@@ -147,18 +147,13 @@ __global__ __launch_bounds__(64 * LD_WAVES) void lora_down_kernel(const void* __
 
 template <int DT, int CT>
 static hipError_t launch_lora_down(const void* x, const __bf16* d, __bf16* o, int M, int K, hipStream_t st) {
-    constexpr int kMaxDev = 64;
-    static bool attr_set[kMaxDev] = {};
+    static std::atomic<bool> attr_set[kMaxDev];
     int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
+    hipError_t e = current_device(&dev);
     if (e != hipSuccess) return e;
-    if (dev < 0 || dev >= kMaxDev) return hipErrorInvalidDevice;
-    if (!attr_set[dev]) {
-        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&lora_down_kernel<DT, CT>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, LoraDownCfg<CT>::LDS);
-        if (e != hipSuccess) return e;
-        attr_set[dev] = true;
-    }
+    e = lds_limit_once(attr_set, dev, reinterpret_cast<const void*>(&lora_down_kernel<DT, CT>),
+                       LoraDownCfg<CT>::LDS);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((lora_down_kernel<DT, CT>), dim3((M + LD_ROWS - 1) / LD_ROWS), dim3(64 * LD_WAVES),
                        LoraDownCfg<CT>::LDS, st, x, d, o, M, K);
     return hipGetLastError();

@@ -687,18 +687,17 @@ __global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
     }
 }
 
-static int g_num_cus = 0;
-
+// Compute units of the current device (256 on MI355X), cached per device.
 static int num_cus() {
-    if (g_num_cus == 0) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-            g_num_cus = n;
-        else
-            g_num_cus = 256;
+    static std::atomic<int> cus[kMaxDev];
+    int dev = 0;
+    if (current_device(&dev) != hipSuccess) return 256;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+        cus[dev].store(n, std::memory_order_relaxed);
     }
-    return g_num_cus;
+    return n;
 }
 
 // Launch shape: a row is np = ceil(K / 1024) passes of 64 lanes; W <= 4 waves
@@ -720,12 +719,12 @@ static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K
     void (*kern)(const void*, int8_t*, float*, int, int) =
         P == 1 ? rotquant_row_kernel<DT, G, 1, OUT> : P == 2 ? rotquant_row_kernel<DT, G, 2, OUT>
         : P == 3 ? rotquant_row_kernel<DT, G, 3, OUT> : rotquant_row_kernel<DT, G, 6, OUT>;   // 5..6 passes: 6
-    static int occupancy[kRowMaxPass + 1][kRowMaxWaves + 1];   // workgroups per CU, per shape
-    int per_cu = occupancy[P][W];
+    static std::atomic<int> occupancy[kRowMaxPass + 1][kRowMaxWaves + 1];   // workgroups per CU, per shape
+    int per_cu = occupancy[P][W].load(std::memory_order_relaxed);
     if (per_cu == 0) {
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64 * W, lds) != hipSuccess || per_cu < 1)
             per_cu = 1;
-        occupancy[P][W] = per_cu;
+        occupancy[P][W].store(per_cu, std::memory_order_relaxed);
     }
     int grid = num_cus() * per_cu;
     if (grid > M) grid = M;

@@ -55,3 +55,49 @@ def test_single_call_vs_oracle(backend, native, oracle, gpu):
     acc = oracle.int_gemm(eqx, qw.cpu().numpy())
     want = oracle.epilogue_f32(acc, exs, ws.cpu().numpy(), b.float().numpy(), out_bf16=True)
     assert np.array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), want)
+
+
+def test_concurrent_host_threads(backend, native, gpu):
+    """Six host threads, each on its own stream, call the single-call linear at
+    once (the library's launch helpers share per-device caches across threads):
+    every call returns the bits of the same call made alone."""
+    import threading
+    cases = [(4608, 3072, 3072), (512, 3072, 12288), (77, 640, 3840), (300, 1024, 9216), (1, 256, 128),
+             (640, 768, 2048)]
+    prepared = []
+    for i, (M, N, K) in enumerate(cases):
+        G = backend.pick_groupsize(K)
+        x = outlier_activations(M, K, seed=40 + i).cuda()
+        qw, ws = backend.quantize_convrot_w4a4_weight(normal_weight(N, K, seed=50 + i).cuda(), convrot_groupsize=G)
+        w6 = backend.prepare_convrot_w4a4_weight_bf6(qw)
+        b = normal_bias(N, seed=60 + i).cuda()
+        want = native.convrot_w4a4_linear_bf6(x, w6, ws, b, None, None, 1.0, native.EPI_BF16, G, N)
+        prepared.append((x, w6, ws, b, G, N, want))
+    torch.cuda.synchronize()
+    got = [None] * len(cases)
+    errors = []
+    start = threading.Barrier(len(cases))
+
+    def run(i):
+        try:
+            x, w6, ws, b, G, N, _ = prepared[i]
+            s = torch.cuda.Stream()
+            start.wait(timeout=60)
+            with torch.cuda.stream(s):
+                outs = [native.convrot_w4a4_linear_bf6(x, w6, ws, b, None, None, 1.0, native.EPI_BF16, G, N)
+                        for _ in range(3)]
+            s.synchronize()
+            got[i] = outs
+        except BaseException as e:          # noqa: BLE001 - reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(len(cases))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=90)
+    assert not errors, errors
+    for i, outs in enumerate(got):
+        assert outs is not None, f"thread {i} did not finish"
+        for y in outs:
+            assert torch.equal(y, prepared[i][6]), cases[i]
