@@ -1,0 +1,56 @@
+"""Seeded sweep of ragged linear shapes through the Linear's forward path
+(convrot_w4a4_linear: fused rotate+quantize, GEMM, dequant epilogue), bf16 and
+f32 activations, with and without bias.  Every bit equals the oracle's: the
+weight quantizer's codes and scales, then rotate+quantize of x, the integer
+GEMM and the f32 epilogue.  K multiples of 128 take the bf6 GEMM, the other
+multiples of 64 the int8-MFMA GEMM (groupsize 256 or 64 as picked from K)."""
+import numpy as np
+import pytest
+import torch
+
+from inputs import bf16_bits, normal_bias, normal_weight, outlier_activations
+
+pytestmark = pytest.mark.gpu
+
+
+def _shapes(n=32, seed=2024):
+    rs = np.random.RandomState(seed)
+    out = []
+    for i in range(n):
+        M = int(rs.choice([1, 2, 3, 7, 31, 33, 64, 100, 255, 257, 300, 513]))
+        N = int(rs.randint(1, 700))
+        K = 64 * int(rs.randint(1, 49))          # 64 .. 3072
+        out.append((M, N, K, "bf16" if i % 3 else "f32", bool(rs.randint(2))))
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,dt,has_bias", _shapes())
+def test_linear_sweep_vs_oracle(backend, oracle, gpu, M, N, K, dt, has_bias):
+    print(f"linear sweep M={M} N={N} K={K} {dt} bias={has_bias}", flush=True)
+    G = backend.pick_groupsize(K)
+    # f32 activations hold bf16-grid values: every fp64 group sum is exact
+    x = outlier_activations(M, K, seed=7 * M + K, dtype=torch.bfloat16)
+    w = normal_weight(N, K, seed=N + K)
+    b = normal_bias(N, seed=N) if has_bias else None
+
+    qw, ws = backend.quantize_convrot_w4a4_weight(w.cuda(), convrot_groupsize=G)
+    eqw, ews = oracle.quantize_weight(w.view(torch.int16).numpy().view(np.uint16), oracle.F16, G)
+    assert np.array_equal(qw.cpu().numpy(), eqw)
+    assert np.array_equal(ws.cpu().numpy().view(np.uint32), ews.view(np.uint32))
+
+    xin = x if dt == "bf16" else x.float()
+    y = backend.convrot_w4a4_linear(xin.cuda(), qw, ws, bias=None if b is None else b.cuda(), convrot_groupsize=G)
+    assert y.shape == (M, N) and y.dtype == xin.dtype
+
+    if dt == "bf16":
+        eqx, exs, _ = oracle.rotquant(bf16_bits(x), oracle.BF16, G)
+    else:
+        eqx, exs, _ = oracle.rotquant(x.float().numpy(), oracle.F32, G)
+    acc = oracle.int_gemm(eqx, eqw)
+    bias32 = None if b is None else b.float().numpy()
+    if dt == "bf16":
+        want = oracle.epilogue_f32(acc, exs, ews, bias32, out_bf16=True)
+        assert np.array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), want)
+    else:
+        want = oracle.epilogue_f32(acc, exs, ews, bias32, out_bf16=False)
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
