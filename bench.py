@@ -96,8 +96,10 @@ class Linear:
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    # 50 untimed steps (about 25 ms of load on the block linears) bring the GPU
+    # to steady clocks: after 5, the next 20 steps still ran 14% slower
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time for the oracle baseline (0 disables it)")
     ap.add_argument("--path", choices=("bf6", "int8", "w8a8"), default="bf6",
