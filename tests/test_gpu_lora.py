@@ -109,7 +109,8 @@ def test_gemm_lora_zero_up_equals_plain_gemm(native, gpu):
                            c.view(torch.int16) if c.dtype == torch.bfloat16 else c)
 
 
-@pytest.mark.parametrize("M,N,K,G", [(77, 256, 3072, 256), (512, 3072, 3072, 256), (40, 200, 1088, 16)])
+@pytest.mark.parametrize("M,N,K,G", [(77, 256, 3072, 256), (512, 3072, 3072, 256), (40, 200, 1088, 16),
+                                     (1, 97, 128, 64), (257, 333, 2048, 256), (5, 1000, 12288, 256)])
 def test_linear_with_fused_lora(backend, native, oracle, gpu, M, N, K, G):
     print(f"linear+lora M={M} N={N} K={K} G={G}", flush=True)
     x = outlier_activations(M, K, seed=M)
