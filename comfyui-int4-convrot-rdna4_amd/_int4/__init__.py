@@ -218,8 +218,15 @@ def convrot_w4a4_linear(
     rotate+quantize of x, then the W4A4 GEMM with the dequant epilogue.  Every
     row count takes the same kernels (the reference's torch-rotation branch
     for M < 512 is not needed: the fused kernel is exact and fast at any M).
-    linear_dtype "int8" computes the same product (the reference routes it to
-    its eager path, whose arithmetic is identical).
+
+    linear_dtype "int8" marks layers the reference sends to its eager path
+    (_int4/__init__.py:104-111 -> _int4/eager.py:172-197), whose output is the
+    eager rounding chain in x's dtype.  Here the same kernels run with that
+    chain as the epilogue: for bf16 x each of acc, *xs, *ws, +bias (and the
+    LoRA term) is rounded to bf16 in turn (_int4/eager.py:162-168); for f32 x
+    the eager chain and the default fp32 epilogue are the same arithmetic.  For
+    f16 x the output is the fp32 epilogue rounded once to f16 (the eager f16
+    chain, which overflows once |acc| > 65504, is not reproduced).
     """
     if linear_dtype not in {"int4", "int8"}:
         raise ValueError(f"ConvRot W4A4 linear_dtype must be 'int4' or 'int8', got {linear_dtype!r}")
@@ -236,8 +243,24 @@ def convrot_w4a4_linear(
     if x2d.dtype not in native._IN_DTYPE_CODE:
         x2d = x2d.to(torch.float32)
     out_dtype = x.dtype if x.dtype in _NATIVE_OUT else torch.float32
-    epi = native.EPI_BF16 if out_dtype == torch.bfloat16 else native.EPI_F32
+    if out_dtype == torch.bfloat16:
+        epi = native.EPI_BF16_EAGER if linear_dtype == "int8" else native.EPI_BF16
+    else:
+        epi = native.EPI_F32
     K, N = x2d.shape[1], qweight.shape[0]
+    if lora is not None:
+        down, up = lora
+        if down.dim() != 2 or up.dim() != 2 or down.shape[1] != K or up.shape[0] != N \
+                or up.shape[1] != down.shape[0]:
+            raise ValueError(f"LoRA shapes D {tuple(down.shape)} U {tuple(up.shape)} do not fit K={K} N={N}")
+        if down.dtype != torch.bfloat16 or up.dtype != torch.bfloat16:
+            raise ValueError(f"LoRA D / U must be bf16, got {down.dtype} / {up.dtype}")
+        if not (down.is_contiguous() and up.is_contiguous()):
+            raise ValueError("LoRA D / U must be contiguous")
+    if wscales.numel() != N:
+        raise ValueError(f"wscales has {wscales.numel()} elements, the weight has N={N} rows")
+    if bias is not None and bias.numel() != N:
+        raise ValueError(f"bias has {bias.numel()} elements, the weight has N={N} rows")
     if bf6_path_ok(K) and x2d.is_cuda and (lora is None or x2d.dtype in (torch.bfloat16, torch.float16)):
         # the whole linear in one library call (same kernels, same bits as the steps below)
         w6 = qweight_bf6 if qweight_bf6 is not None else prepare_convrot_w4a4_weight_bf6(qweight)
@@ -253,8 +276,6 @@ def convrot_w4a4_linear(
         down = up = None
         if lora is not None:
             down, up = lora
-            if down.shape[1] != K or up.shape[0] != N or up.shape[1] != down.shape[0]:
-                raise ValueError(f"LoRA shapes D {tuple(down.shape)} U {tuple(up.shape)} do not fit K={K} N={N}")
         native._check_cuda(x2d, w6, wsc, b32, down, up)
         out = native.convrot_w4a4_linear_bf6(native._aligned(x2d), w6, wsc, b32, down, up, 1.0, epi,
                                              convrot_groupsize, N)
@@ -264,8 +285,6 @@ def convrot_w4a4_linear(
     t = up = None
     if lora is not None:
         down, up = lora
-        if down.shape[1] != K or up.shape[0] != N or up.shape[1] != down.shape[0]:
-            raise ValueError(f"LoRA shapes D {tuple(down.shape)} U {tuple(up.shape)} do not fit K={K} N={N}")
         xd = x2d if x2d.dtype in (torch.bfloat16, torch.float16) else x2d.to(torch.bfloat16)
         t = native.lora_down(xd, down)
     if bf6_path_ok(K):
@@ -280,7 +299,7 @@ def convrot_w4a4_linear(
     else:
         qact, x_scale = native.convrot_quant_int4(x2d, convrot_groupsize)
         if t is None:
-            out = native.int4_convrot_gemm(qact, qweight, x_scale, wscales, bias, out_dtype)
+            out = native.int4_convrot_gemm_ex(qact, qweight, x_scale, wscales, bias, epi)
         else:
             out = native.int4_convrot_gemm_lora(qact, qweight, x_scale, wscales, bias, t, up, 1.0, epi)
     if out.dtype != x.dtype:

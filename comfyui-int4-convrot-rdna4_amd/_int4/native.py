@@ -28,10 +28,14 @@ _IN_DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
 EPI_F32, EPI_BF16, EPI_BF16_EAGER, EPI_ACC = 0, 1, 2, 3
 
+# cr_abi_version() of the library these signatures describe
+ABI_VERSION = 7
+
 _vp, _i = ctypes.c_void_p, ctypes.c_int
 _SIGNATURES = {
     "ck_convrot_quant_int4": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
     "ck_int4_convrot_gemm": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
+    "ck_int4_convrot_gemm_splitk": ([_vp] * 5 + [_i] * 4 + [_vp], _i),
     "cr_int4_convrot_gemm_ex": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
     "cr_convrot_quant_int4_stochastic": ([_vp, _i, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
     "cr_lora_down": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
@@ -78,6 +82,11 @@ def load_library():
                 f"{os.path.basename(path)} is not built; run the package's _int4/build.py "
                 "(hipcc --offload-arch=gfx950) first")
         lib = ctypes.CDLL(path)
+        ver = lib.cr_abi_version
+        ver.argtypes, ver.restype = [], _i
+        if ver() != ABI_VERSION:
+            raise RuntimeError(f"{os.path.basename(path)} has ABI version {ver()}, these bindings need "
+                               f"{ABI_VERSION}; rebuild it with the package's _int4/build.py")
         for name, (args, res) in _SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = args
@@ -232,6 +241,25 @@ def int4_convrot_gemm(x_packed, w_packed, x_scale, w_scale, bias, out_dtype):
     if rc != 0:
         raise RuntimeError(f"ck_int4_convrot_gemm failed, hipError={rc}")
     return out
+
+
+def int4_convrot_gemm_splitk(x_packed, w_packed, x_scale, w_scale, nsplit: int):
+    """Split-K form (reference hip_loader.py:176-192): returns the f32 [M, N]
+    product (Xint @ Wint^T) * x_scale[:,None] * w_scale[None,:] without bias,
+    accumulated by ck_int4_convrot_gemm_splitk into a zeroed buffer.  Bit-
+    identical to int4_convrot_gemm(..., bias=None, float32) for every nsplit."""
+    if nsplit < 1:
+        raise ValueError(f"nsplit must be >= 1, got {nsplit}")
+    lib = load_library()
+    x_packed, w_packed, x_scale, w_scale, _, M, N, K = _gemm_args(x_packed, w_packed, x_scale, w_scale, None)
+    if x_scale is None or w_scale is None or x_scale.numel() != M or w_scale.numel() != N:
+        raise ValueError("x_scale [M] and w_scale [N] are required")
+    accum = torch.zeros((M, N), dtype=torch.float32, device=x_packed.device)
+    rc = lib.ck_int4_convrot_gemm_splitk(_ptr(x_packed), _ptr(w_packed), _ptr(x_scale), _ptr(w_scale), _ptr(accum),
+                                         M, N, K, nsplit, _stream(x_packed.device))
+    if rc != 0:
+        raise RuntimeError(f"ck_int4_convrot_gemm_splitk failed, hipError={rc}")
+    return accum
 
 
 def lora_down(x: torch.Tensor, down: torch.Tensor) -> torch.Tensor:

@@ -33,6 +33,8 @@ hipError_t int8_to_i8t_launch(const void* src, void* dst, int rows, int K, hipSt
 hipError_t gemm_i8t_launch(const int8_t* X, const int8_t* W, const float* xs, const float* ws,
                            const float* bias, void* out, int M, int N, int K, int epi, hipStream_t st);
 size_t gemm_bf6_splitk_workspace(int M, int N, int nsplit);
+hipError_t gemm_splitk_launch(const int8_t* Xp, const int8_t* Wp, const float* xs, const float* ws, float* accum,
+                              int M, int N, int K, int nsplit, hipStream_t st);
 }  // namespace convrot
 
 #define API extern "C" __attribute__((visibility("default")))
@@ -80,6 +82,15 @@ API int ck_int4_convrot_gemm(const void* Xp, const void* Wp, const void* xscale,
                              void* stream) {
     if (out_dtype != 0 && out_dtype != 1) return -1;
     return cr_int4_convrot_gemm_ex(Xp, Wp, xscale, wscale, bias, out, M, N, K, out_dtype, stream);
+}
+
+API int ck_int4_convrot_gemm_splitk(const void* Xp, const void* Wp, const void* xscale, const void* wscale,
+                                    void* accum, int M, int N, int K, int nsplit, void* stream) {
+    if (K % 32 != 0 || K <= 0 || K >= 131072 || M < 0 || N < 0 || nsplit < 1) return -1;
+    return (int)convrot::gemm_splitk_launch(reinterpret_cast<const int8_t*>(Xp), reinterpret_cast<const int8_t*>(Wp),
+                                            reinterpret_cast<const float*>(xscale),
+                                            reinterpret_cast<const float*>(wscale), reinterpret_cast<float*>(accum),
+                                            M, N, K, nsplit, reinterpret_cast<hipStream_t>(stream));
 }
 
 static int lora_rank_ok(int R) { return R >= 32 && R <= 128 && R % 32 == 0; }
@@ -268,4 +279,4 @@ API int cr_convrot_w4a4_linear_bf6(const void* x, int in_dtype, const void* W6, 
 
 API int cr_max_quant_k(void) { return convrot::rotquant_max_k(); }
 
-API int cr_abi_version(void) { return 6; }
+API int cr_abi_version(void) { return 7; }

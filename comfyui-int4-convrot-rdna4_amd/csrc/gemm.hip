@@ -62,7 +62,10 @@ __global__ __launch_bounds__(NTHR) void w4a4_gemm_kernel(
     const int m0 = blockIdx.y * TBM;
     const int n0 = blockIdx.x * TBN;
     const int Kb = I8 ? K : K / 2;       // operand bytes per row
-    const int nkb = (Kb + ROWB - 1) / ROWB;
+    // k range of this workgroup: split blockIdx.z of gridDim.z (1 unless split-K)
+    const int nkb_all = (Kb + ROWB - 1) / ROWB;
+    const int kb_begin = (int)((long long)blockIdx.z * nkb_all / gridDim.z);
+    const int kb_end = (int)((long long)(blockIdx.z + 1) * nkb_all / gridDim.z);
 
     // global -> LDS staging: (TBM + TBN) rows x 4 chunks of 16 B = 2048 chunks, 4 per lane
     uint4 stage[4];
@@ -102,16 +105,16 @@ __global__ __launch_bounds__(NTHR) void w4a4_gemm_kernel(
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = (v16i){0};
 
-    gload(0);
+    gload(kb_begin);
     lstore(0);
     __syncthreads();
 
     const int frow = lane & 31;          // fragment row within a 32-row tile
     const int fhalf = lane >> 5;         // which 16-byte half of a 32-byte k slice
 
-    for (int kb = 0; kb < nkb; ++kb) {
-        const int buf = kb & 1;
-        if (kb + 1 < nkb) gload(kb + 1);
+    for (int kb = kb_begin; kb < kb_end; ++kb) {
+        const int buf = (kb - kb_begin) & 1;
+        if (kb + 1 < kb_end) gload(kb + 1);
         const uint8_t* la = &lds[buf][0];
         const uint8_t* lb = &lds[buf][TBM * LDS_STRIDE];
 #pragma unroll
@@ -152,7 +155,7 @@ __global__ __launch_bounds__(NTHR) void w4a4_gemm_kernel(
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a_hi[i], b_hi[j], acc[i][j], 0, 0, 0);
                 }
         }
-        if (kb + 1 < nkb) lstore(buf ^ 1);
+        if (kb + 1 < kb_end) lstore(buf ^ 1);
         __syncthreads();
     }
 
@@ -210,7 +213,11 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
     const int m0 = tm * P_BM;
     const int n0 = tn * P_BN;
     const int Kb = I8 ? K : K / 2;                      // operand bytes per row
-    const int nkb = Kb / P_ROWB;
+    const int nkb_all = Kb / P_ROWB;
+    // k range of this workgroup: split blockIdx.y of gridDim.y (1 unless split-K);
+    // every split holds at least one block (the launch keeps gridDim.y <= nkb_all)
+    const int kb_begin = (int)((long long)blockIdx.y * nkb_all / gridDim.y);
+    const int nkb = (int)((long long)(blockIdx.y + 1) * nkb_all / gridDim.y) - kb_begin;
     float* sc = reinterpret_cast<float*>(plds + P_STAGES * P_STAGE_BYTES);
     stage_scales(sc, xs, ws, bias, M, N, m0, n0, tid, 128 * WN);   // visible after the loop's first barrier
 
@@ -218,7 +225,8 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
     // DMA source rows / chunks for this lane's P_LOADS instructions (fixed per tile)
     const int8_t* src[P_LOADS];
     if constexpr (TM) {   // waves 0..3 copy the A chunk, waves 4..7 the B chunk, 1 KB per instruction
-        const int8_t* base = wave < 4 ? Xp + (size_t)tm * nkb * I8T_CHUNK : Wp + (size_t)tn * nkb * I8T_CHUNK;
+        const int8_t* base = (wave < 4 ? Xp + (size_t)tm * nkb_all * I8T_CHUNK : Wp + (size_t)tn * nkb_all * I8T_CHUNK)
+                             + (size_t)kb_begin * I8T_CHUNK;
 #pragma unroll
         for (int j = 0; j < P_LOADS; ++j) src[j] = base + ((wave & 3) * P_LOADS + j) * 1024 + lane * 16;
     } else
@@ -229,10 +237,10 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
         const int c = swz(r, slot & 3);                      // logical chunk stored at this slot
         if (r < P_BM) {
             const int gm = min(m0 + r, M - 1);
-            src[j] = Xp + (size_t)gm * Kb + c * 16;
+            src[j] = Xp + (size_t)gm * Kb + (size_t)kb_begin * P_ROWB + c * 16;
         } else {
             const int gn = min(n0 + (r - P_BM), N - 1);
-            src[j] = Wp + (size_t)gn * Kb + c * 16;
+            src[j] = Wp + (size_t)gn * Kb + (size_t)kb_begin * P_ROWB + c * 16;
         }
     }
     const uint32_t lds_base = (uint32_t)(uintptr_t)plds;
@@ -425,11 +433,14 @@ __global__ __launch_bounds__(128 * WN) void w4a4_gemm_pipe_kernel(
                                          n0 + wn * WTN_P, lane, lora, plds + wave * SCR);
 }
 
+// nsplit > 1 (EPI_ATOMIC_ACC only): the k blocks are split over nsplit
+// workgroups per tile, at most one split per k block.
 template <int EPI, bool LORA, bool I8 = false, bool TM = false>
 static hipError_t launch_epi(const int8_t* Xp, const int8_t* Wp, const float* xs, const float* ws,
                              const float* bias, void* out, int M, int N, int K, const LoraArgs& la,
-                             hipStream_t st) {
-    if (TM || (I8 ? K : K / 2) % P_ROWB == 0) {
+                             hipStream_t st, int nsplit = 1) {
+    const int Kb = I8 ? K : K / 2;
+    if (TM || Kb % P_ROWB == 0) {
         constexpr int WN = CONVROT_PIPE_WN;
         const int ntiles = ((M + P_BM - 1) / P_BM) * ((N + P_BN - 1) / P_BN);
         static std::atomic<bool> attr_set[kMaxDev];
@@ -439,11 +450,13 @@ static hipError_t launch_epi(const int8_t* Xp, const int8_t* Wp, const float* xs
         e = lds_limit_once(attr_set, dev,
                            reinterpret_cast<const void*>(&w4a4_gemm_pipe_kernel<EPI, WN, LORA, I8, TM>), P_LDS_BYTES);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<EPI, WN, LORA, I8, TM>), dim3(ntiles), dim3(128 * WN),
+        const int splits = min(nsplit, Kb / P_ROWB);
+        hipLaunchKernelGGL((w4a4_gemm_pipe_kernel<EPI, WN, LORA, I8, TM>), dim3(ntiles, splits), dim3(128 * WN),
                            P_LDS_BYTES, st, Xp, Wp, xs, ws, bias, out, M, N, K, la,
                            tile_group_rows((M + P_BM - 1) / P_BM));
     } else if constexpr (!TM) {
-        dim3 grid((N + TBN - 1) / TBN, (M + TBM - 1) / TBM), block(NTHR);
+        const int splits = min(nsplit, (Kb + ROWB - 1) / ROWB);
+        dim3 grid((N + TBN - 1) / TBN, (M + TBM - 1) / TBM, splits), block(NTHR);
         hipLaunchKernelGGL((w4a4_gemm_kernel<EPI, LORA, I8>), grid, block, 0, st, Xp, Wp, xs, ws, bias, out, M, N, K, la);
     }
     return hipGetLastError();
@@ -513,6 +526,37 @@ hipError_t int8_to_i8t_launch(const void* src, void* dst, int rows, int K, hipSt
     const long long threads = (long long)((rows + 255) / 256) * (K / 64) * 1024;
     hipLaunchKernelGGL(int8_to_i8t_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
                        reinterpret_cast<const int8_t*>(src), reinterpret_cast<int8_t*>(dst), rows, K);
+    return hipGetLastError();
+}
+
+// Split-K finalize: accum holds the exact int32 accumulators (the sum of every
+// split's partial); each becomes fl32(fl32(float(acc) * xs[m]) * ws[n]) in
+// place, the unsplit f32 epilogue without its bias term.
+__global__ __launch_bounds__(256) void splitk_finalize_kernel(float* __restrict__ accum, const float* __restrict__ xs,
+                                                              const float* __restrict__ ws, int M, int N) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long long)M * N) return;
+    const int m = (int)(i / N), n = (int)(i - (long long)m * N);
+    const int acc = __float_as_int(accum[i]);
+    accum[i] = __fmul_rn(__fmul_rn((float)acc, xs[m]), ws[n]);
+}
+
+// The reference's split-K contract (_int4/int4_gemm.hip:259-330, 634-645):
+// accum f32 [M, N] arrives zeroed; afterwards it holds the scaled product
+// without bias.  Here each split adds its exact integer partial (the int32
+// view of the zeroed buffer starts at 0), and the finalize scales the total
+// once, so the result is the unsplit f32 epilogue bit for bit for every
+// nsplit (the reference adds separately rounded float partials).
+hipError_t gemm_splitk_launch(const int8_t* Xp, const int8_t* Wp, const float* xs, const float* ws, float* accum,
+                              int M, int N, int K, int nsplit, hipStream_t st) {
+    if (M == 0 || N == 0) return hipSuccess;
+    const LoraArgs none{nullptr, nullptr, 0, 0.0f};
+    hipError_t e = launch_epi<EPI_ATOMIC_ACC, false>(Xp, Wp, nullptr, nullptr, nullptr, accum, M, N, K, none, st,
+                                                     nsplit);
+    if (e != hipSuccess) return e;
+    const long long n = (long long)M * N;
+    hipLaunchKernelGGL(splitk_finalize_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, accum, xs, ws, M,
+                       N);
     return hipGetLastError();
 }
 

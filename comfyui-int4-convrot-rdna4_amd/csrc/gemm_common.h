@@ -12,7 +12,10 @@ namespace convrot {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-enum : int { EPI_F32 = 0, EPI_BF16 = 1, EPI_BF16_EAGER = 2, EPI_ACC = 3 };
+// EPI_ATOMIC_ACC: the k-split partial of the packed split-K entry point; the
+// exact integer accumulator of the workgroup's k range is added atomically
+// into an int32 [M, N] buffer (integer sums are exact in any order).
+enum : int { EPI_F32 = 0, EPI_BF16 = 1, EPI_BF16_EAGER = 2, EPI_ACC = 3, EPI_ATOMIC_ACC = 4 };
 
 __device__ __forceinline__ float bf16r(float f) { return round_to_dt<DT_BF16>(f); }
 
@@ -88,7 +91,7 @@ __device__ __forceinline__ void epilogue_tiles(const AccV (&acc)[FMT][FNT], cons
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int row = rbase + 8 * (r >> 2) + (r & 3);
-            xsv[r] = (EPI != EPI_ACC && row < M) ? xs[row] : 0.0f;
+            xsv[r] = (EPI != EPI_ACC && EPI != EPI_ATOMIC_ACC && row < M) ? xs[row] : 0.0f;
         }
 #pragma unroll
         for (int j = 0; j < FNT; ++j) {
@@ -107,7 +110,7 @@ __device__ __forceinline__ void epilogue_tiles(const AccV (&acc)[FMT][FNT], cons
             }
             if (col >= N) continue;
             float wsc = 0.0f, bv = 0.0f;
-            if constexpr (EPI != EPI_ACC) {
+            if constexpr (EPI != EPI_ACC && EPI != EPI_ATOMIC_ACC) {
                 wsc = ws[col];
                 if (bias) bv = bias[col];
             }
@@ -119,6 +122,8 @@ __device__ __forceinline__ void epilogue_tiles(const AccV (&acc)[FMT][FNT], cons
                 const size_t o = (size_t)row * N + col;
                 if constexpr (EPI == EPI_ACC) {
                     reinterpret_cast<int32_t*>(out)[o] = a;
+                } else if constexpr (EPI == EPI_ATOMIC_ACC) {
+                    atomicAdd(reinterpret_cast<int32_t*>(out) + o, a);
                 } else if constexpr (EPI == EPI_BF16_EAGER) {
                     float v = bf16r(bf16r((float)a) * bf16r(xsv[r]));
                     v = bf16r(v * bf16r(wsc));
@@ -197,7 +202,7 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
     }
     // per-lane column scales and biases of the 4 quads of each column tile
     float wv[FNT][4][4], bvv[FNT][4][4];
-    if constexpr (EPI != EPI_ACC) {
+    if constexpr (EPI != EPI_ACC && EPI != EPI_ATOMIC_ACC) {
 #pragma unroll
         for (int j = 0; j < FNT; ++j)
 #pragma unroll
@@ -250,7 +255,7 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     uint8_t* dst = scr + (ii * 32 + l32) * RS + (j * 32 + 8 * q + 4 * h) * ES;
-                    if constexpr (EPI == EPI_ACC) {
+                    if constexpr (EPI == EPI_ACC || EPI == EPI_ATOMIC_ACC) {
                         *reinterpret_cast<int4*>(dst) = make_int4(acc_int<ASH>(acc[i][j][4 * q]), acc_int<ASH>(acc[i][j][4 * q + 1]),
                                                                   acc_int<ASH>(acc[i][j][4 * q + 2]), acc_int<ASH>(acc[i][j][4 * q + 3]));
                     } else {
@@ -298,7 +303,12 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
             uint8_t* o = orow + (size_t)(q0 / 64) * RSTEP * N * ES;
             if (row < M && col < N) {
                 const uint4 d = *reinterpret_cast<const uint4*>(scr + rl * RS + cc * 16);
-                if (vec && col + EPC <= N) {
+                if constexpr (EPI == EPI_ATOMIC_ACC) {     // one atomic add per int32 accumulator
+                    const uint32_t w[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (col + e < N) atomicAdd(reinterpret_cast<int32_t*>(o) + e, (int32_t)w[e]);
+                } else if (vec && col + EPC <= N) {
                     *reinterpret_cast<uint4*>(o) = d;
                 } else {
                     const uint32_t w[4] = {d.x, d.y, d.z, d.w};

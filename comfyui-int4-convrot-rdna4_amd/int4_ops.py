@@ -1,14 +1,22 @@
 """INT4 ConvRot-W4A4 custom operations for ComfyUI on AMD MI355X (gfx950).
 
 ``Int4ConvRotOps`` is the drop-in for the reference's class of the same name
-(reference ``int4_ops.py:44-386``): a ``comfy.ops.manual_cast`` subclass whose
-``Linear`` quantizes weights to packed int4 at load time (or loads prequantized
-ones) and runs the forward through the gfx950 W4A4 kernels.  The class
-attributes the loader sets, the per-layer attributes the Save node reads
-(``_q``, ``_qs``, ``_qgs``, ``_qmode``, ``_dyn_lora``) and the
-``_load_from_state_dict`` dispatch order (prequantized -> LoRA -> quantize ->
-plain load) are those of the reference, so its loader and Save nodes use this
-class unchanged.
+(reference ``int4_ops.py:44-386``).  What the interface fixes is kept: the
+``comfy.ops.manual_cast`` base, the class attributes the loader sets
+(``int4_loader.py:221-259``), the per-layer attributes the Save node reads
+(``_q``, ``_qs``, ``_qgs``, ``_qmode``, ``_dyn_lora``; ``int4_save.py:110-130``),
+the method names other code calls, and the order in which a layer's state is
+resolved at load time:
+
+  1. a prequantized weight (int8 tensor + ``weight_scale``) is taken as stored;
+  2. LoRA patches for the layer either stay a forward-time bypass (dynamic mode,
+     layers that will be quantized) or are folded into the float weight/bias;
+  3. an eligible float weight is quantized on the GPU from its fp16 copy;
+  4. anything else loads as a plain ``manual_cast`` layer.
+
+The forward runs every quantized layer through the gfx950 kernels of
+``_int4`` (one library call per linear); plain LoRA bypasses are concatenated
+into one low-rank pair that the GEMM epilogue adds.
 """
 import json
 import logging
@@ -38,7 +46,14 @@ try:
 except Exception:  # pragma: no cover
     _WA_BASE = None
 
+# container prefixes stripped from state-dict keys before they are matched
+# against LoRA key maps and the loader's exact-key sets
 _KEY_PREFIXES = ("diffusion_model.", "model.diffusion_model.", "model.", "transformer.")
+
+# the attributes ComfyUI's BypassForwardHook gives an adapter wrapped around a
+# Linear; h() reads them
+_LINEAR_BYPASS_ATTRS = {"is_conv": False, "conv_dim": 0, "kernel_size": (1,), "in_channels": None,
+                        "out_channels": None, "kw_dict": {}}
 
 
 def hip_backend_ready() -> bool:
@@ -46,20 +61,45 @@ def hip_backend_ready() -> bool:
 
 
 def _strip_prefix(key):
-    if not isinstance(key, str):
-        return key
-    for p in _KEY_PREFIXES:
-        if key.startswith(p):
-            return key[len(p):]
+    if isinstance(key, str):
+        for p in _KEY_PREFIXES:
+            if key.startswith(p):
+                return key[len(p):]
     return key
 
 
 def _patch_fields(patch):
     """(v, offset, function[, strength]) -> (v, offset, function, strength)."""
-    if len(patch) == 4:
-        return patch
-    v, offset, function = patch
-    return v, offset, function, 1.0
+    v, offset, function, *rest = patch
+    return v, offset, function, (rest[0] if rest else 1.0)
+
+
+def _has_additive_bypass(v) -> bool:
+    """Whether adapter v adds a term h(x) to the layer output without needing
+    the base weight: LoRA / LoHa / LoKr do; raw diff/set tuples, adapters
+    that keep the base class's zero h() (OFT/BOFT) and DoRA (a LoRA with a
+    dora_scale) do not."""
+    if not (hasattr(v, "weights") and hasattr(v, "h")):
+        return False
+    if _WA_BASE is not None and type(v).h is _WA_BASE.h:
+        return False
+    w = v.weights
+    dora = getattr(v, "name", None) == "lora" and isinstance(w, (tuple, list)) and len(w) > 4 \
+        and w[4] is not None
+    return not dora
+
+
+def _arm_bypass(v, strength):
+    """Make adapter v callable as a Linear bypass: its float tensors in fp16 on
+    the GPU, and the attributes h() reads."""
+    w = v.weights
+    if isinstance(w, (tuple, list)):
+        v.weights = tuple(t.to("cuda", torch.float16) if torch.is_tensor(t) and t.is_floating_point() else t
+                          for t in w)
+    v.multiplier = float(strength)
+    for name, value in _LINEAR_BYPASS_ATTRS.items():
+        setattr(v, name, value)
+    return v
 
 
 def _plain_lora(v, in_features, out_features):
@@ -103,6 +143,29 @@ def _parse_quant_tag(tag):
     return True, (int(conf.get("convrot_groupsize", 0)) or None)
 
 
+class _Keys:
+    """The state-dict keys of one layer."""
+    __slots__ = ("prefix", "weight", "scale", "bias", "tag")
+
+    def __init__(self, prefix):
+        self.prefix = prefix
+        self.weight, self.scale = prefix + "weight", prefix + "weight_scale"
+        self.bias, self.tag = prefix + "bias", prefix + "comfy_quant"
+
+
+def _meta_skeleton(mod, in_features, out_features, bias, dtype):
+    """A Linear with meta-device parameters: the loader builds the model this
+    way only to discover the LoRA key map, so no storage is allocated."""
+    nn.Module.__init__(mod)
+    mod.in_features, mod.out_features = in_features, out_features
+    spec = {"device": "meta"} if dtype is None else {"device": "meta", "dtype": dtype}
+    shapes = [("weight", (out_features, in_features))] + ([("bias", (out_features,))] if bias else [])
+    for name, shape in shapes:
+        setattr(mod, name, nn.Parameter(torch.empty(shape, **spec), requires_grad=False))
+    if not bias:
+        mod.bias = None
+
+
 if _COMFY_OPS and _CK_OK:
 
     class Int4ConvRotOps(manual_cast):
@@ -123,97 +186,56 @@ if _COMFY_OPS and _CK_OK:
 
         class Linear(manual_cast.Linear):
             def __init__(self, in_features, out_features, bias=True, device=None, dtype=None):
-                if getattr(Int4ConvRotOps, "skeleton_meta_init", False):
-                    # meta-device skeleton used only for LoRA key-map discovery
-                    nn.Module.__init__(self)
-                    self.in_features = in_features
-                    self.out_features = out_features
-                    kw = {"device": "meta"}
-                    if dtype is not None:
-                        kw["dtype"] = dtype
-                    self.weight = nn.Parameter(torch.empty((out_features, in_features), **kw),
-                                               requires_grad=False)
-                    self.bias = (nn.Parameter(torch.empty((out_features,), **kw), requires_grad=False)
-                                 if bias else None)
+                if Int4ConvRotOps.skeleton_meta_init:
+                    _meta_skeleton(self, in_features, out_features, bias, dtype)
                 else:
                     super().__init__(in_features, out_features, bias, device, dtype)
-                self._q = None        # int8: packed [N, K/2] (int4) or plain [N, K] (int8)
-                self._qs = None       # per-row scale f32 [N]
-                self._qgs = None      # convrot groupsize
-                self._qmode = None    # "int4" | "int8" | None (bf16)
-                self._q6 = None       # int4 weight re-encoded for the bf6 matrix-core GEMM (load time)
-                self._q8t = None      # int8 weight re-laid for the tile-major W8A8 GEMM (load time)
-                self._dyn_lora = None
-                self._dyn_fused = None   # (D, U) bf16: plain LoRAs fused into the GEMM epilogue
-                self._dyn_rest = None    # adapters that keep the generic h() side path
+                # quantized storage (None: a plain layer)
+                self._q = self._qs = self._qgs = self._qmode = None
+                self._q6 = None       # int4 weight as the bf6 GEMM's operand (made at load time)
+                self._q8t = None      # int8 weight as the tile-major W8A8 GEMM's operand
+                # dynamic LoRA: every attached adapter, the plain ones fused into one
+                # (D, U) pair for the GEMM epilogue, and the rest (h() side path)
+                self._dyn_lora = self._dyn_fused = self._dyn_rest = None
                 self.comfy_cast_weights = False
 
             _normalize_lora_key = staticmethod(_strip_prefix)
 
             @staticmethod
             def _format_lora_patches(patches):
-                """-> (strength, v, key_strength, offset, function) tuples of comfy.lora."""
-                out = []
-                for p in patches or []:
-                    v, offset, function, strength = _patch_fields(p)
-                    out.append((strength, v, 1.0, offset, function))
-                return out
+                """-> the (strength, v, key_strength, offset, function) entries
+                comfy.lora.calculate_weight takes."""
+                return [(s, v, 1.0, off, fn) for v, off, fn, s in map(_patch_fields, patches or [])]
+
+            @staticmethod
+            def _patches_for(key):
+                nk = _strip_prefix(key)
+                return nk, Int4ConvRotOps.lora_patches.get(nk)
 
             def _apply_lora(self, tensor, key):
-                """Fold the LoRA patches registered for `key` into `tensor`."""
-                if tensor is None or tensor.dtype == torch.int8 or not Int4ConvRotOps.lora_patches:
-                    return tensor
-                nk = _strip_prefix(key)
-                patches = Int4ConvRotOps.lora_patches.get(nk)
-                if not patches:
+                """`tensor` with the LoRA patches registered for `key` folded in
+                (the same tensor object when there are none)."""
+                nk, patches = self._patches_for(key)
+                if tensor is None or tensor.dtype == torch.int8 or not patches:
                     return tensor
                 import comfy.lora
                 import comfy.model_management
-                dev = tensor.device
-                if dev.type == "cpu" and torch.cuda.is_available():
-                    dev = torch.device("cuda")
-                t = tensor.to(device=dev, dtype=comfy.model_management.lora_compute_dtype(dev))
-                merged = comfy.lora.calculate_weight(self._format_lora_patches(patches), t, key)
+                dev = torch.device("cuda") if tensor.device.type == "cpu" and torch.cuda.is_available() \
+                    else tensor.device
+                work = tensor.to(dev, comfy.model_management.lora_compute_dtype(dev))
+                baked = comfy.lora.calculate_weight(self._format_lora_patches(patches), work, key)
                 Int4ConvRotOps._applied_lora.add(nk)
-                return merged.to(dtype=tensor.dtype)
+                return baked.to(tensor.dtype)
 
-            @staticmethod
-            def _dyn_capable(v):
-                """True for adapters with an additive bypass h(x) (LoRA/LoHa/LoKr),
-                false for raw diff/set patches, DoRA and OFT/BOFT."""
-                if not hasattr(v, "weights") or not hasattr(v, "h"):
-                    return False
-                if _WA_BASE is not None and type(v).h is _WA_BASE.h:
-                    return False
-                w = getattr(v, "weights", None)
-                is_dora = (getattr(v, "name", None) == "lora" and isinstance(w, (tuple, list))
-                           and len(w) > 4 and w[4] is not None)
-                return not is_dora
+            _dyn_capable = staticmethod(_has_additive_bypass)
 
             def _prepare_dyn_adapters(self, patches):
-                """Turn patches into forward-time bypass adapters (fp16 on the GPU).
-                Returns None when one of them cannot run as a side path."""
-                prepared = []
-                for p in patches or []:
-                    v, _offset, _function, strength = _patch_fields(p)
-                    if not self._dyn_capable(v):
-                        return None
-                    w = getattr(v, "weights", None)
-                    if isinstance(w, (tuple, list)):
-                        v.weights = tuple(
-                            t.to(device="cuda", dtype=torch.float16)
-                            if isinstance(t, torch.Tensor) and t.is_floating_point() else t
-                            for t in w)
-                    # the attributes comfy's BypassForwardHook would set for a Linear
-                    v.multiplier = float(strength)
-                    v.is_conv = False
-                    v.conv_dim = 0
-                    v.kernel_size = (1,)
-                    v.in_channels = None
-                    v.out_channels = None
-                    v.kw_dict = {}
-                    prepared.append(v)
-                return prepared
+                """The patches as armed bypass adapters, or None when one of them
+                has no additive bypass (the layer then bakes instead)."""
+                fields = [_patch_fields(p) for p in patches or []]
+                if not all(_has_additive_bypass(v) for v, *_ in fields):
+                    return None
+                return [_arm_bypass(v, strength) for v, _, _, strength in fields]
 
             def _set_dyn_lora(self, prepared):
                 """Attach prepared adapters; the plain LoRAs among them are
@@ -222,7 +244,7 @@ if _COMFY_OPS and _CK_OK:
                 self._dyn_lora = prepared
                 self._dyn_fused, self._dyn_rest = None, prepared
                 plain = [_plain_lora(v, self.in_features, self.out_features) for v in prepared]
-                if not any(p is not None for p in plain):
+                if all(p is None for p in plain):
                     return
                 try:
                     fused = _ck.fuse_lora_pairs([p for p in plain if p is not None])
@@ -233,8 +255,20 @@ if _COMFY_OPS and _CK_OK:
                     self._dyn_fused = fused
                     self._dyn_rest = [v for v, p in zip(prepared, plain) if p is None]
 
+            def _attach_dyn_lora(self, wkey, patches=None):
+                """Attach the layer's patches as bypass adapters.  Returns False
+                when they cannot all run that way."""
+                nk, found = self._patches_for(wkey)
+                patches = found if patches is None else patches
+                prepared = self._prepare_dyn_adapters(patches) if patches else None
+                if prepared is None:
+                    return False
+                self._set_dyn_lora(prepared)
+                Int4ConvRotOps._applied_lora.add(nk)
+                return True
+
             def _apply_dyn_lora(self, x, out, adapters=None):
-                """out + sum of the attached adapters' h(x) (already scaled)."""
+                """out plus each adapter's bypass term h(x) (already scaled)."""
                 for v in (self._dyn_lora if adapters is None else adapters) or ():
                     try:
                         out = out + v.h(x, out)
@@ -247,162 +281,145 @@ if _COMFY_OPS and _CK_OK:
                 return _strip_prefix(prefix[:-1] if prefix.endswith(".") else prefix)
 
             def _should_quantize(self, prefix, w):
-                if not Int4ConvRotOps.enable or w is None or w.dim() != 2:
+                ops = Int4ConvRotOps
+                eligible = (ops.enable and w is not None and w.dim() == 2
+                            and self.in_features >= ops.min_in_features
+                            and _pick_groupsize(self.in_features) is not None)
+                if not eligible or any(n in prefix for n in ops.excluded_names or ()):
                     return False
-                if self.in_features < Int4ConvRotOps.min_in_features:
-                    return False
-                if _pick_groupsize(self.in_features) is None:
-                    return False
-                if any(n in prefix for n in (Int4ConvRotOps.excluded_names or [])):
-                    return False
-                return self._exact_key(prefix) not in Int4ConvRotOps.excluded_exact
+                return self._exact_key(prefix) not in ops.excluded_exact
 
             def _quant_mode(self, prefix):
                 return "int8" if self._exact_key(prefix) in Int4ConvRotOps.int8_exact else "int4"
 
-            def _take_bias(self, state_dict, prefix, dev):
-                bkey = prefix + "bias"
-                if bkey in state_dict:
-                    self.bias = nn.Parameter(state_dict.pop(bkey).to(dev, torch.float16),
-                                             requires_grad=False)
+            # -- load-time state ------------------------------------------------
 
-            def _attach_dyn_lora(self, wkey):
-                nk = _strip_prefix(wkey)
-                patches = Int4ConvRotOps.lora_patches.get(nk)
-                if patches:
-                    prepared = self._prepare_dyn_adapters(patches)
-                    if prepared is not None:
-                        self._set_dyn_lora(prepared)
-                        Int4ConvRotOps._applied_lora.add(nk)
+            def _install(self, q, scale, groupsize, mode, state_dict, keys, consumed):
+                """Take over quantized storage (on the GPU): the checkpoint copy,
+                the GEMM operand made from it, and the bias in fp16; the
+                `consumed` keys leave state_dict."""
+                dev = torch.device("cuda")
+                self._q = q.to(dev).contiguous()
+                self._qs = scale.to(dev, torch.float32).reshape(-1).contiguous()
+                self._qgs, self._qmode = groupsize, mode
+                self._q6 = _ck.prepare_convrot_w4a4_weight_bf6(self._q) if mode == "int4" else None
+                self._q8t = _ck.prepare_convrot_w8a8_weight_i8t(self._q) if mode == "int8" else None
+                self.weight = None
+                for k in consumed:
+                    state_dict.pop(k, None)
+                if keys.bias in state_dict:
+                    self.bias = nn.Parameter(state_dict.pop(keys.bias).to(dev, torch.float16), requires_grad=False)
 
             def _load_prequantized(self, state_dict, prefix, wkey, skey, w):
                 """Load a packed int4 (cols == K/2) or int8 (cols == K) ConvRot
                 weight as stored (legacy header files or ComfyUI native files
                 with a comfy_quant tag).  Returns True if consumed."""
                 cols = w.shape[-1]
-                if cols == self.in_features:
-                    mode = "int8"
-                elif cols * 2 == self.in_features:
-                    mode = "int4"
-                else:
+                mode = "int8" if cols == self.in_features else "int4" if 2 * cols == self.in_features else None
+                if mode is None:
                     return False
-                qkey = prefix + "comfy_quant"
-                gs = None
-                tag = state_dict.get(qkey, None)
-                if tag is not None:
+                keys = _Keys(prefix)
+                groupsize = None
+                if keys.tag in state_dict:
                     try:
-                        ok, gs = _parse_quant_tag(tag)
-                        if not ok:
-                            return False
+                        accepted, groupsize = _parse_quant_tag(state_dict[keys.tag])
                     except Exception:
-                        gs = None
-                if gs is None:
-                    gs = _pick_groupsize(self.in_features)
-                if gs is None:
+                        accepted = True          # unreadable tag: decide from in_features
+                    if not accepted:
+                        return False
+                groupsize = groupsize or _pick_groupsize(self.in_features)
+                if groupsize is None:
                     return False
-                dev = torch.device("cuda")
-                self._q = w.to(dev).contiguous()
-                self._qs = state_dict[skey].to(dev, torch.float32).reshape(-1).contiguous()
-                self._qgs, self._qmode = gs, mode
-                self._q6 = _ck.prepare_convrot_w4a4_weight_bf6(self._q) if mode == "int4" else None
-                self._q8t = _ck.prepare_convrot_w8a8_weight_i8t(self._q) if mode == "int8" else None
-                self.weight = None
-                for k in (wkey, skey, qkey):
-                    state_dict.pop(k, None)
-                self._take_bias(state_dict, prefix, dev)
+                self._install(w, state_dict[skey], groupsize, mode, state_dict, keys,
+                              (keys.weight, keys.scale, keys.tag))
                 if Int4ConvRotOps.lora_dynamic and Int4ConvRotOps.lora_patches:
                     self._attach_dyn_lora(wkey)
                 return True
 
+            def _take_prequantized(self, state_dict, keys, w):
+                if w is None or w.dtype != torch.int8 or keys.scale not in state_dict:
+                    return False
+                try:
+                    return self._load_prequantized(state_dict, keys.prefix, keys.weight, keys.scale, w)
+                except Exception as e:
+                    logging.warning(f"INT4 ConvRot: prequant load failed for {keys.prefix}, "
+                                    f"falling back to bf16: {e}")
+                    return False
+
+            def _route_lora(self, state_dict, keys, w):
+                """Dynamic bypass for a layer about to be quantized, else fold
+                the patches into the float weight and bias in state_dict.
+                Returns the (possibly patched) weight."""
+                if not Int4ConvRotOps.lora_patches:
+                    return w
+                _, patches = self._patches_for(keys.weight)
+                floating = w is not None and w.dtype != torch.int8
+                if (Int4ConvRotOps.lora_dynamic and patches and floating
+                        and self._should_quantize(keys.prefix, w) and self._attach_dyn_lora(keys.weight, patches)):
+                    return w
+                for key, t in ((keys.weight, w if floating else None), (keys.bias, state_dict.get(keys.bias))):
+                    patched = self._apply_lora(t, key)
+                    if patched is not t:
+                        state_dict[key] = patched
+                return state_dict.get(keys.weight, w)
+
+            def _quantize_on_load(self, state_dict, keys, w):
+                if not self._should_quantize(keys.prefix, w):
+                    return False
+                mode = self._quant_mode(keys.prefix)
+                groupsize = _pick_groupsize(self.in_features)
+                w16 = w.to("cuda", torch.float16)        # the loader's quantization input dtype
+                try:
+                    if mode == "int8":
+                        from ._int4.int8_eager import quantize_convrot_w8a8_weight
+                        q, s = quantize_convrot_w8a8_weight(w16, convrot_groupsize=groupsize)
+                    else:
+                        seed = Int4ConvRotOps._STOCHASTIC_SEED if Int4ConvRotOps.lora_mode == "Stochastic" else 0
+                        q, s = _ck.quantize_convrot_w4a4_weight(w16, convrot_groupsize=groupsize,
+                                                                stochastic_rounding=seed)
+                    self._install(q, s, groupsize, mode, state_dict, keys, (keys.weight,))
+                    return True
+                except Exception as e:
+                    logging.warning(f"INT4 ConvRot: fell back to bf16 for {keys.prefix}: {e}")
+                    return False
+
             def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict,
                                       missing_keys, unexpected_keys, error_msgs):
-                wkey, skey = prefix + "weight", prefix + "weight_scale"
-                w = state_dict.get(wkey, None)
-
-                # (1) prequantized checkpoint
-                if w is not None and w.dtype == torch.int8 and skey in state_dict:
-                    try:
-                        if self._load_prequantized(state_dict, prefix, wkey, skey, w):
-                            return
-                    except Exception as e:
-                        logging.warning(f"INT4 ConvRot: prequant load failed for {prefix}, "
-                                        f"falling back to bf16: {e}")
-
-                # LoRA: dynamic side path for layers that will be quantized, else bake
-                if Int4ConvRotOps.lora_patches:
-                    nk = _strip_prefix(wkey)
-                    wpatches = Int4ConvRotOps.lora_patches.get(nk)
-                    prepared = None
-                    if (Int4ConvRotOps.lora_dynamic and wpatches and w is not None
-                            and w.dtype != torch.int8 and self._should_quantize(prefix, w)):
-                        prepared = self._prepare_dyn_adapters(wpatches)
-                    if prepared is not None:
-                        self._set_dyn_lora(prepared)
-                        Int4ConvRotOps._applied_lora.add(nk)
-                    else:
-                        if w is not None and w.dtype != torch.int8:
-                            wp = self._apply_lora(w, wkey)
-                            if wp is not w:
-                                w = wp
-                                state_dict[wkey] = w
-                        bkey = prefix + "bias"
-                        b = state_dict.get(bkey, None)
-                        if b is not None:
-                            bp = self._apply_lora(b, bkey)
-                            if bp is not b:
-                                state_dict[bkey] = bp
-
-                # (2) quantize on the fly from an fp16 copy on the GPU
-                if self._should_quantize(prefix, w):
-                    dev = torch.device("cuda")
-                    gs = _pick_groupsize(self.in_features)
-                    mode = self._quant_mode(prefix)
-                    try:
-                        if mode == "int8":
-                            from ._int4.int8_eager import quantize_convrot_w8a8_weight
-                            qw, ws = quantize_convrot_w8a8_weight(w.to(dev, torch.float16), convrot_groupsize=gs)
-                        else:
-                            stoch = (Int4ConvRotOps._STOCHASTIC_SEED
-                                     if Int4ConvRotOps.lora_mode == "Stochastic" else 0)
-                            qw, ws = _ck.quantize_convrot_w4a4_weight(
-                                w.to(dev, torch.float16), convrot_groupsize=gs, stochastic_rounding=stoch)
-                        self._q, self._qs, self._qgs, self._qmode = qw, ws.float(), gs, mode
-                        self._q6 = _ck.prepare_convrot_w4a4_weight_bf6(qw) if mode == "int4" else None
-                        self._q8t = _ck.prepare_convrot_w8a8_weight_i8t(qw) if mode == "int8" else None
-                        self.weight = None
-                        state_dict.pop(wkey, None)
-                        self._take_bias(state_dict, prefix, dev)
-                        return
-                    except Exception as e:
-                        logging.warning(f"INT4 ConvRot: fell back to bf16 for {prefix}: {e}")
-
-                # (3) plain load
+                keys = _Keys(prefix)
+                w = state_dict.get(keys.weight)
+                if self._take_prequantized(state_dict, keys, w):
+                    return
+                w = self._route_lora(state_dict, keys, w)
+                if self._quantize_on_load(state_dict, keys, w):
+                    return
                 return super()._load_from_state_dict(
                     state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys, error_msgs)
+
+            # -- forward ---------------------------------------------------------
+
+            def _to_device(self, dev):
+                """Move the quantized storage to `dev` once (the loader may keep
+                layers elsewhere until the model runs)."""
+                if self._q.device == dev:
+                    return
+                self._q, self._qs = self._q.to(dev), self._qs.to(dev)
+                self._q6 = None if self._q6 is None else self._q6.to(dev)
+                self._q8t = None if self._q8t is None else self._q8t.to(dev)
+                if self._dyn_fused is not None:
+                    self._dyn_fused = tuple(t.to(dev) for t in self._dyn_fused)
 
             def forward(self, x):
                 if self._q is None:
                     return self._apply_dyn_lora(x, super().forward(x))
-                if self._q.device != x.device:
-                    self._q = self._q.to(x.device)
-                    self._qs = self._qs.to(x.device)
-                    if self._q6 is not None:
-                        self._q6 = self._q6.to(x.device)
-                    if self._q8t is not None:
-                        self._q8t = self._q8t.to(x.device)
-                bias = self.bias
-                if bias is not None and bias.device != x.device:
-                    bias = bias.to(x.device)
+                self._to_device(x.device)
+                bias = self.bias if self.bias is None or self.bias.device == x.device else self.bias.to(x.device)
                 if self._qmode == "int8":
-                    out = _ck.convrot_w8a8_linear(x, self._q, self._qs, bias=bias,
-                                                  convrot_groupsize=self._qgs, qweight_i8t=self._q8t)
-                    return self._apply_dyn_lora(x, out)
-                fused = self._dyn_fused
-                if fused is not None and fused[0].device != x.device:
-                    fused = self._dyn_fused = (fused[0].to(x.device), fused[1].to(x.device))
-                out = _ck.convrot_w4a4_linear(x, self._q, self._qs, bias=bias, convrot_groupsize=self._qgs,
-                                              lora=fused, qweight_bf6=self._q6)
-                return self._apply_dyn_lora(x, out, self._dyn_rest if fused is not None else None)
+                    y = _ck.convrot_w8a8_linear(x, self._q, self._qs, bias=bias, convrot_groupsize=self._qgs,
+                                                qweight_i8t=self._q8t)
+                    return self._apply_dyn_lora(x, y)
+                y = _ck.convrot_w4a4_linear(x, self._q, self._qs, bias=bias, convrot_groupsize=self._qgs,
+                                            lora=self._dyn_fused, qweight_bf6=self._q6)
+                return self._apply_dyn_lora(x, y, None if self._dyn_fused is None else self._dyn_rest)
 
 else:  # comfy.ops or the backend unavailable
     Int4ConvRotOps = None

@@ -3,8 +3,11 @@
  *
  * Library: comfyui-int4-convrot-rdna4_amd/_int4/libconvrot_gfx950.so
  *
- * Conventions (the same as the reference's ctypes boundary, so its bindings
- * load this library unchanged; reference _int4/hip_loader.py:42-71):
+ * Conventions: those of the reference's ctypes boundary.  The five exports the
+ * reference's loader binds (_int4/hip_loader.py:42-71: ck_int4_convrot_gemm,
+ * ck_int4_convrot_gemm_splitk, ck_convrot_quant_int4, ck_int8_convrot_gemm,
+ * ck_convrot_quant_int8) exist here with the same names, argument lists and
+ * contracts, so that loader binds this library unchanged:
  *   - all pointers are device pointers; the caller allocates every buffer
  *     (outputs included); the library holds no device memory;
  *   - work is enqueued asynchronously on `stream` (a hipStream_t, e.g.
@@ -52,6 +55,25 @@ int ck_convrot_quant_int4(const void* x, int in_dtype, void* qout, void* scaleou
 int ck_int4_convrot_gemm(const void* Xp, const void* Wp, const void* xscale, const void* wscale,
                          const void* bias, void* out, int M, int N, int K, int out_dtype,
                          void* stream);
+
+/*
+ * Split-K form of ck_int4_convrot_gemm for small output grids (the reference
+ * chooses it for few tiles and large K, _int4/hip_loader.py:20-36).
+ *   accum f32 [M, N], zeroed by the caller; on return it holds
+ *   fl32(fl32(acc * xscale[m]) * wscale[n]), the scaled product WITHOUT bias;
+ *   the caller adds the bias and casts (_int4/hip_loader.py:176-192).
+ * The k blocks are split over min(nsplit, ceil(K / 128)) workgroups per tile;
+ * each adds its exact integer partial into accum (viewed as int32, which is 0
+ * for a zeroed float buffer) with atomics, and one more kernel scales the sum
+ * in place.  The result is therefore bit-identical to ck_int4_convrot_gemm's
+ * f32 epilogue (bias NULL) for every nsplit.  A non-zeroed accum gives
+ * undefined results.  K % 32 == 0, nsplit >= 1; otherwise -1.
+ * Replaces: ck_int4_convrot_gemm_splitk, reference _int4/int4_gemm.hip:634-645
+ * (bound at _int4/hip_loader.py:53-56, called at :176-192), whose partials are
+ * rounded per split and added in an order the atomics decide.
+ */
+int ck_int4_convrot_gemm_splitk(const void* Xp, const void* Wp, const void* xscale, const void* wscale,
+                                void* accum, int M, int N, int K, int nsplit, void* stream);
 
 /*
  * ck_int4_convrot_gemm with an explicit epilogue:
@@ -155,11 +177,11 @@ int cr_int4_convrot_gemm_bf6_lora(const void* A6, const void* W6, const void* xs
  *   t == NULL: no LoRA term, epilogue 0..3; else LoRA as cr_int4_convrot_gemm_bf6_lora
  *   (epilogue 0..2).  1 <= nsplit <= K / 128; nsplit == 1 needs no workspace,
  *   otherwise workspace_bytes >= cr_gemm_bf6_splitk_workspace(M, N, nsplit).
- * Replaces: ck_int4_convrot_gemm_splitk, reference _int4/int4_gemm.hip:634-645
- * (chosen by _choose_nsplit, _int4/hip_loader.py:20-36, called at :176-190),
- * which adds rounded fp32 partials into a zeroed [M, N] buffer with atomics and
- * leaves bias and cast to torch; this one owns its workspace layout and
- * finishes the epilogue itself.
+ * The bf6 counterpart of ck_int4_convrot_gemm_splitk (reference
+ * _int4/int4_gemm.hip:634-645, which adds rounded fp32 partials into a zeroed
+ * [M, N] buffer with atomics and leaves bias and cast to torch): this one owns
+ * its workspace layout, sums the partials in a fixed order and finishes the
+ * epilogue itself.
  */
 int cr_int4_convrot_gemm_bf6_splitk(const void* A6, const void* W6, const void* xscale, const void* wscale,
                                     const void* bias, const void* t, const void* U, int R, float scale,

@@ -40,9 +40,58 @@ def test_library_exports_every_declared_symbol(native):
     assert set(native.exported_symbols()) == set(header_symbols())
 
 
+# What the reference's ctypes loader binds, name by name, with the argtypes it
+# installs (reference _int4/hip_loader.py:50-71): pointers (c_void_p) and ints.
+REFERENCE_BINDINGS = {
+    "ck_int4_convrot_gemm": [ctypes.c_void_p] * 6 + [ctypes.c_int] * 4 + [ctypes.c_void_p],
+    "ck_int4_convrot_gemm_splitk": [ctypes.c_void_p] * 5 + [ctypes.c_int] * 4 + [ctypes.c_void_p],
+    "ck_convrot_quant_int4": [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                              ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p],
+    "ck_int8_convrot_gemm": [ctypes.c_void_p] * 6 + [ctypes.c_int] * 4 + [ctypes.c_void_p],
+    "ck_convrot_quant_int8": [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                              ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p],
+}
+
+
+def test_reference_loader_binds_this_library(native):
+    """The reference loader's _ensure_loaded resolves all five symbols
+    unconditionally; each must exist with an int return and the same argument
+    list as in the header (same count and kinds), and reject bad arguments
+    with -1 exactly as the reference does, before touching the device."""
+    lib = ctypes.CDLL(native.lib_path())
+    text = open(os.path.join(ROOT, "include", "convrot_mi355x.h")).read()
+    for name, argtypes in REFERENCE_BINDINGS.items():
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_int
+        fn.argtypes = argtypes
+        decl = re.search(r"^int\s+" + name + r"\s*\(([^;]*)\);", text, flags=re.M | re.S)
+        assert decl, name
+        params = [a.strip() for a in decl.group(1).split(",")]
+        assert len(params) == len(argtypes), name
+        for p, t in zip(params, argtypes):
+            assert ("*" in p) == (t is ctypes.c_void_p), (name, p)
+    n = None
+    assert lib.ck_int4_convrot_gemm(n, n, n, n, n, n, 4, 4, 48, 1, n) == -1          # K % 32
+    assert lib.ck_int4_convrot_gemm_splitk(n, n, n, n, n, 4, 4, 48, 2, n) == -1     # K % 32
+    assert lib.ck_int4_convrot_gemm_splitk(n, n, n, n, n, 4, 4, 64, 0, n) == -1     # nsplit < 1
+    assert lib.ck_int4_convrot_gemm_splitk(n, n, n, n, n, 0, 4, 64, 2, n) == 0      # empty: nothing to do
+    assert lib.ck_convrot_quant_int4(n, 1, n, n, 4, 256, 32, n) == -1              # G not 16/64/256
+    assert lib.ck_int8_convrot_gemm(n, n, n, n, n, n, 4, 4, 40, 1, n) == -1          # K % 16
+    assert lib.ck_convrot_quant_int8(n, 1, n, n, 4, 100, 16, n) == -1              # K % G
+
+
+def test_load_refuses_other_abi_version(native, monkeypatch):
+    """Bindings for another ABI version refuse the library instead of calling
+    it with mismatched arguments."""
+    monkeypatch.setattr(native, "_lib", None)
+    monkeypatch.setattr(native, "ABI_VERSION", native.ABI_VERSION + 1)
+    with pytest.raises(RuntimeError, match="ABI version"):
+        native.load_library()
+
+
 def test_library_queries_without_gpu(native):
     lib = native.load_library()
-    assert lib.cr_abi_version() == 6
+    assert lib.cr_abi_version() == native.ABI_VERSION == 7
     assert lib.cr_max_quant_k() == 32768
     assert lib.cr_max_quant_bf6_k() == 12288
 
@@ -115,6 +164,19 @@ def test_linear_validation_errors(backend):
     with pytest.raises(ValueError):
         backend.convrot_w4a4_linear(torch.zeros(4, 80, dtype=torch.bfloat16),
                                     torch.zeros(8, 40, dtype=torch.int8), ws, convrot_groupsize=256)
+    qw = torch.zeros(8, 256, dtype=torch.int8)
+    with pytest.raises(ValueError, match="wscales"):                 # N scales
+        backend.convrot_w4a4_linear(x, qw, torch.ones(7))
+    with pytest.raises(ValueError, match="bias"):                    # N biases
+        backend.convrot_w4a4_linear(x, qw, ws, bias=torch.zeros(9))
+    D = torch.zeros(32, 512, dtype=torch.bfloat16)
+    U = torch.zeros(8, 32, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="bf16"):                    # LoRA dtype
+        backend.convrot_w4a4_linear(x, qw, ws, lora=(D.half(), U))
+    with pytest.raises(ValueError, match="contiguous"):              # LoRA layout
+        backend.convrot_w4a4_linear(x, qw, ws, lora=(D, torch.zeros(32, 8, dtype=torch.bfloat16).T))
+    with pytest.raises(ValueError, match="LoRA shapes"):
+        backend.convrot_w4a4_linear(x, qw, ws, lora=(D, torch.zeros(8, 64, dtype=torch.bfloat16)))
 
 
 def test_weight_validation_errors(backend):
@@ -225,3 +287,52 @@ def test_split_choice_and_workspace(native):
     assert lib.cr_gemm_bf6_choose_nsplit(256, 256, 256) <= 2
     assert lib.cr_gemm_bf6_splitk_workspace(512, 3072, 4) == 4 * 24 * 256 * 256 * 4
     assert lib.cr_gemm_bf6_splitk_workspace(300, 300, 1) == 0
+
+
+def test_ops_meta_skeleton(ops_mod):
+    """skeleton_meta_init builds meta-device parameters (the loader's LoRA
+    key-map discovery pass) with the quantized-state attributes unset."""
+    Ops = ops_mod.Int4ConvRotOps
+    Ops.skeleton_meta_init = True
+    try:
+        a = Ops.Linear(3072, 64, bias=True, dtype=torch.bfloat16)
+        b = Ops.Linear(3072, 64, bias=False)
+    finally:
+        Ops.skeleton_meta_init = False
+    assert a.weight.device.type == "meta" and a.weight.shape == (64, 3072) and a.weight.dtype == torch.bfloat16
+    assert a.bias.device.type == "meta" and a.bias.shape == (64,)
+    assert b.bias is None and b.weight.device.type == "meta"
+    for m in (a, b):
+        assert m._q is None and m._qs is None and m._qgs is None and m._qmode is None and m._dyn_lora is None
+        assert m.in_features == 3072 and m.out_features == 64
+
+
+def test_ops_lora_routing_without_quantization(ops_mod):
+    """A layer that stays bf16 folds its LoRA patches into weight and bias
+    (through comfy.lora.calculate_weight) even in dynamic mode; patches of
+    adapters without an additive bypass are refused for the side path."""
+    import comfy
+    calls = []
+
+    def calculate_weight(patches, t, key):
+        calls.append((key, [p[0] for p in patches]))
+        return t + 1.0
+    comfy.lora = types.SimpleNamespace(calculate_weight=calculate_weight)
+    comfy.model_management = types.SimpleNamespace(lora_compute_dtype=lambda dev: torch.float32)
+    sys.modules["comfy.lora"], sys.modules["comfy.model_management"] = comfy.lora, comfy.model_management
+    Ops = ops_mod.Int4ConvRotOps
+    Ops.lora_patches = {"blk.lin.weight": [("patch", None, None, 0.5)], "blk.lin.bias": [("patch", None, None)]}
+    Ops.lora_dynamic = True
+    try:
+        lin = Ops.Linear(256, 32, bias=True)                  # narrower than min_in_features: stays bf16
+        sd = {"diffusion_model.blk.lin.weight": torch.zeros(32, 256), "diffusion_model.blk.lin.bias": torch.zeros(32)}
+        lin._load_from_state_dict(sd, "diffusion_model.blk.lin.", {}, True, [], [], [])
+        assert lin._q is None and lin._dyn_lora is None
+        assert torch.equal(lin.weight, torch.ones(32, 256)) and torch.equal(lin.bias, torch.ones(32))
+        assert calls == [("diffusion_model.blk.lin.weight", [0.5]), ("diffusion_model.blk.lin.bias", [1.0])]
+        assert Ops._applied_lora == {"blk.lin.weight", "blk.lin.bias"}
+        assert lin._prepare_dyn_adapters([("raw diff tensor", None, None, 1.0)]) is None
+    finally:
+        Ops.lora_patches, Ops.lora_dynamic, Ops._applied_lora = {}, False, set()
+        for k in ("comfy.lora", "comfy.model_management"):
+            sys.modules.pop(k, None)

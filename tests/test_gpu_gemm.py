@@ -87,3 +87,31 @@ def test_bf16_output_close_to_eager_chain(native, oracle, gpu):
     out = native.int4_convrot_gemm(cu(xp), cu(wp), cu(xs), cu(ws), cu(b), torch.bfloat16)
     got = out.float().cpu().numpy().astype(np.float64)
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) <= 1e-2
+
+
+# the reference's split-K export: pipelined kernel (K % 128 == 0) and the
+# register-staged one (K % 128 != 0), nsplit below, at and above the k-block count
+SPLITK_CASES = [(64, 256, 3072, [1, 2, 8, 24, 40]), (300, 200, 160, [1, 2, 3]), (257, 513, 12288, [3, 8, 96]),
+                (8, 1000, 3840, [2, 7, 30]), (512, 3072, 12288, [8])]
+
+
+@pytest.mark.parametrize("M,N,K,splits", SPLITK_CASES)
+def test_reference_splitk_bitexact(native, oracle, gpu, M, N, K, splits):
+    """ck_int4_convrot_gemm_splitk: the zeroed f32 accumulator ends up holding
+    fl32(fl32(acc * xs) * ws) for every nsplit: against the oracle's epilogue
+    (sampled rows) and bit-identical to the unsplit f32 epilogue without bias;
+    bias + cast afterwards (as the reference's caller does) gives the unsplit
+    bf16 output."""
+    print(f"ck splitk M={M} N={N} K={K}", flush=True)
+    xp, wp, xs, ws, b = rand_case(M, N, K, 11 * M + K)
+    args = (cu(xp), cu(wp), cu(xs), cu(ws))
+    base = native.int4_convrot_gemm(*args, None, torch.float32)
+    rows = np.arange(M) if M <= 300 else np.random.RandomState(5).choice(M, 16, replace=False)
+    ref = oracle.epilogue_f32(oracle.int_gemm(xp[rows], wp), xs[rows], ws, None)
+    assert np.array_equal(base.cpu().numpy()[rows].view(np.uint32), ref.view(np.uint32))
+    for s in splits:
+        acc = native.int4_convrot_gemm_splitk(*args, s)
+        assert torch.equal(acc.view(torch.int32), base.view(torch.int32)), s
+    bf = (acc + cu(b)).to(torch.bfloat16)
+    unsplit = native.int4_convrot_gemm(*args, cu(b), torch.bfloat16)
+    assert torch.equal(bf.view(torch.int16), unsplit.view(torch.int16))
