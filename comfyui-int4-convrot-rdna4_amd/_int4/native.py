@@ -29,7 +29,7 @@ _IN_DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 EPI_F32, EPI_BF16, EPI_BF16_EAGER, EPI_ACC = 0, 1, 2, 3
 
 # cr_abi_version() of the library these signatures describe
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _vp, _i = ctypes.c_void_p, ctypes.c_int
 _SIGNATURES = {
@@ -58,6 +58,8 @@ _SIGNATURES = {
     "cr_convrot_w4a4_linear_bf6": ([_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _i, ctypes.c_float, _vp] + [_i] * 5
                                    + [_vp, ctypes.c_size_t, _vp], _i),
     "cr_convrot_w4a4_linear_bf6_workspace": ([_i, _i, _i, _i], ctypes.c_size_t),
+    "cr_convrot_w4a4_linear_bf6_noalloc": ([_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _i, ctypes.c_float, _vp] + [_i] * 5
+                                           + [_vp], _i),
     "cr_max_quant_k": ([], _i),
     "cr_abi_version": ([], _i),
 }

@@ -252,17 +252,19 @@ API size_t cr_convrot_w4a4_linear_bf6_workspace(int M, int N, int K, int R) {
     return lin_plan(M, N, K, R).total;
 }
 
-API int cr_convrot_w4a4_linear_bf6(const void* x, int in_dtype, const void* W6, const void* wscale, const void* bias,
-                                   int bias_dtype, const void* D, const void* U, int R, float scale, void* out,
-                                   int epilogue, int M, int N, int K, int G, void* workspace, size_t workspace_bytes,
-                                   void* stream) {
-    if (!quant_args_ok(in_dtype, M, K, G) || !bf6_k_ok(K) || K > convrot::rotquant_b6_max_k() || N < 0) return -1;
-    if (bias_dtype < 0 || bias_dtype > 2) return -1;
-    if (epilogue < 0 || epilogue > 2) return -1;
-    if (R != 0 && (!lora_rank_ok(R) || D == nullptr || U == nullptr || in_dtype == 0)) return -1;
-    if (M == 0 || N == 0) return 0;
-    const LinPlan p = lin_plan(M, N, K, R);
-    if (workspace == nullptr || workspace_bytes < p.total) return -1;
+static int linear_bf6_args_ok(int in_dtype, int bias_dtype, const void* D, const void* U, int R, int epilogue,
+                              int M, int N, int K, int G) {
+    if (!quant_args_ok(in_dtype, M, K, G) || !bf6_k_ok(K) || K > convrot::rotquant_b6_max_k() || N < 0) return 0;
+    if (bias_dtype < 0 || bias_dtype > 2) return 0;
+    if (epilogue < 0 || epilogue > 2) return 0;
+    if (R != 0 && (!lora_rank_ok(R) || D == nullptr || U == nullptr || in_dtype == 0)) return 0;
+    return 1;
+}
+
+// The linear's launches with its intermediates at `workspace` (p.total bytes).
+static int linear_bf6_run(const void* x, int in_dtype, const void* W6, const void* wscale, const void* bias,
+                          int bias_dtype, const void* D, const void* U, int R, float scale, void* out, int epilogue,
+                          int M, int N, int K, int G, const LinPlan& p, void* workspace, void* stream) {
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
     float* xs = reinterpret_cast<float*>(ws + p.xs);
@@ -277,6 +279,64 @@ API int cr_convrot_w4a4_linear_bf6(const void* x, int in_dtype, const void* W6, 
                                          ws + p.part, st);
 }
 
+API int cr_convrot_w4a4_linear_bf6(const void* x, int in_dtype, const void* W6, const void* wscale, const void* bias,
+                                   int bias_dtype, const void* D, const void* U, int R, float scale, void* out,
+                                   int epilogue, int M, int N, int K, int G, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+    if (!linear_bf6_args_ok(in_dtype, bias_dtype, D, U, R, epilogue, M, N, K, G)) return -1;
+    if (M == 0 || N == 0) return 0;
+    const LinPlan p = lin_plan(M, N, K, R);
+    if (workspace == nullptr || workspace_bytes < p.total) return -1;
+    return linear_bf6_run(x, in_dtype, W6, wscale, bias, bias_dtype, D, U, R, scale, out, epilogue, M, N, K, G, p,
+                          workspace, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free form of cr_convrot_w4a4_linear_bf6.  The intermediates live
+// in `scratch`, a file-scope device array of kScratchBytes that every GPU the
+// library runs on holds until the process ends.  In host code `scratch` names
+// a host-side stand-in, so its device address is looked up once per device
+// (hipGetSymbolAddress with that device current, on the first call there) and
+// only that address is passed to kernels.  Nothing here allocates; every byte
+// the kernels read from the scratch is written earlier in the same call
+// (codes and padding rows, scales, LoRA t, split partials), so nothing needs
+// clearing between calls.  Calls that overlap on one GPU share the array and
+// race.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+static hipError_t scratch_address(void** out) {
+    static std::atomic<void*> addr[convrot::kMaxDev];
+    int dev = 0;
+    hipError_t e = convrot::current_device(&dev);
+    if (e != hipSuccess) return e;
+    void* p = addr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (p == nullptr) return hipErrorInvalidSymbol;
+        addr[dev].store(p, std::memory_order_release);
+    }
+    *out = p;
+    return hipSuccess;
+}
+
+API int cr_convrot_w4a4_linear_bf6_noalloc(const void* x, int in_dtype, const void* W6, const void* wscale,
+                                           const void* bias, int bias_dtype, const void* D, const void* U, int R,
+                                           float scale, void* out, int epilogue, int M, int N, int K, int G,
+                                           void* stream) {
+    if (!linear_bf6_args_ok(in_dtype, bias_dtype, D, U, R, epilogue, M, N, K, G)) return -1;
+    if (M == 0 || N == 0) return 0;
+    const LinPlan p = lin_plan(M, N, K, R);
+    if (p.total > kScratchBytes) return -1;       // this shape needs more than the library's scratch
+    void* ws = nullptr;
+    hipError_t e = scratch_address(&ws);
+    if (e != hipSuccess) return (int)e;
+    return linear_bf6_run(x, in_dtype, W6, wscale, bias, bias_dtype, D, U, R, scale, out, epilogue, M, N, K, G, p, ws,
+                          stream);
+}
+
 API int cr_max_quant_k(void) { return convrot::rotquant_max_k(); }
 
-API int cr_abi_version(void) { return 7; }
+API int cr_abi_version(void) { return 8; }

@@ -217,6 +217,27 @@ int cr_convrot_w4a4_linear_bf6(const void* x, int in_dtype, const void* W6, cons
 size_t cr_convrot_w4a4_linear_bf6_workspace(int M, int N, int K, int R);
 
 /*
+ * cr_convrot_w4a4_linear_bf6 without the workspace argument: the library
+ * allocates nothing during the call (no hipMalloc, no allocating library
+ * routine).  The intermediates live in a 64 MiB device array that the library
+ * holds on every GPU it runs on until the process ends; the caller passes
+ * inputs and outputs only.  Same kernels, same bits as
+ * cr_convrot_w4a4_linear_bf6.  Returns -1 (no device work) when the shape's
+ * cr_convrot_w4a4_linear_bf6_workspace(M, N, K, R) exceeds 64 MiB (e.g. M =
+ * 4608 fits for K <= 12288; M = 16384, K = 12288 does not), and for the same
+ * argument errors as cr_convrot_w4a4_linear_bf6.  The array is shared by all
+ * calls on one GPU and holds the last call's contents: calls that overlap on
+ * one GPU (different streams, or host threads) race.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory during a forward (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).
+ */
+int cr_convrot_w4a4_linear_bf6_noalloc(const void* x, int in_dtype, const void* W6, const void* wscale,
+                                       const void* bias, int bias_dtype, const void* D, const void* U, int R,
+                                       float scale, void* out, int epilogue, int M, int N, int K, int G,
+                                       void* stream);
+
+/*
  * W8A8 tier (the reference's int8 ConvRot layers, _int4/int8_eager.py).
  *
  * Fused ConvRot rotation + rowwise int8 quantization:
