@@ -701,19 +701,24 @@ static int num_cus() {
 }
 
 // Launch shape: a row is np = ceil(K / 1024) passes of 64 lanes; W <= 4 waves
-// of a workgroup share it with P = ceil(np / W) passes each: one pass per wave
-// up to np = 4, 2 or 3 passes up to np = 8, else 2 waves of 5..6 passes.
-// Measured at M = 4608: K = 3072 3 waves x 1 pass 16.2 us (1 x 3: 17.7,
-// 2 x 2: 16.7); K = 12288 2 x 6 48.9 us (4 x 3: 52.1, 3 x 4: 54.9, 6 x 2:
-// 65.2, 12 x 1: 54.7).  The grid is the number of workgroups that fit on the
-// chip at once, lowered so that every workgroup walks the same number of rows.
+// of a workgroup share it with P = ceil(np / W) passes each.  Rows of up to 4
+// passes (K <= 4096) go to one wave each (W = 1, P = np): no barrier between
+// waves, and the per-row tail (absmax, scale) is paid once per np passes.
+// Longer rows: 2 or 3 passes per wave up to np = 8, else 2 waves of 5..6
+// passes.  Measured (HIP events, bf16 -> B6T): M = 4608, K = 3072: 1 wave x 3
+// passes 17.2 us, 3 x 1 18.3 us; M = 16384, K = 3072: 1 x 3 42.5 us, 3 x 1
+// 52.2 us; M = 4608, K = 12288: 2 x 6 51.1 us, 1 x 12 54.0 us.  The grid is the
+// number of workgroups that fit on the chip at once, lowered so that every
+// workgroup walks the same number of rows.
 template <int DT, int G, int OUT>
 static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K, hipStream_t st) {
     if (M <= 0) return hipSuccess;
     const int np = (K / kChunk + 63) / 64;
-    int P = np <= kRowMaxWaves ? 1 : np <= 2 * kRowMaxWaves ? (np % 3 != 0 ? 2 : 3) : (np + 1) / 2;
+    int P = np <= kRowMaxWaves ? np : np <= 2 * kRowMaxWaves ? (np % 3 != 0 ? 2 : 3) : (np + 1) / 2;
+    if (P == 4) P = 6;                    // 4-pass rows: the 6-pass kernel, its last two passes idle
     int W = (np + P - 1) / P;
     P = (np + W - 1) / W;
+    if (P == 4 || P == 5) P = 6;
     if (W > kRowMaxWaves || P > kRowMaxPass) return hipErrorInvalidValue;
     const size_t lds = (size_t)W * kRowWaveLds + 16 * sizeof(float);
     void (*kern)(const void*, int8_t*, float*, int, int) =
@@ -726,6 +731,11 @@ static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K
             per_cu = 1;
         occupancy[P][W].store(per_cu, std::memory_order_relaxed);
     }
+    // Single-wave workgroups: as many as the LDS holds per CU (160 KB on gfx950),
+    // even where the occupancy query reports fewer; the surplus queues behind
+    // the resident ones.  Measured at M = 4608, K = 3072: one row per workgroup
+    // 17.2 us, two 19.3 us; at M = 16384: four rows 42.5 us, eight 50.2 us.
+    if (W == 1) per_cu = per_cu > (int)((160u << 10) / lds) ? per_cu : (int)((160u << 10) / lds);
     int grid = num_cus() * per_cu;
     if (grid > M) grid = M;
     const int rows = (M + grid - 1) / grid;
