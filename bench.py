@@ -107,10 +107,12 @@ def main():
                          "W8A8 tier (int8 activations and weights on int8 MFMA)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (counter calibration)")
-    ap.add_argument("--workload", choices=("block-linears", "dit8", "gemm-sweep"), default="block-linears",
+    ap.add_argument("--workload", choices=("block-linears", "dit8", "gemm-sweep", "rotquant"),
+                    default="block-linears",
                     help="block-linears: the four linears of one DiT block (the headline line); "
                          "dit8: the synthetic 8-block double-stream DiT stack through Int4ConvRotOps; "
-                         "gemm-sweep: the W4A4 GEMM alone over a token sweep (k-split as the Linear chooses)")
+                         "gemm-sweep: the W4A4 GEMM alone over a token sweep (k-split as the Linear chooses); "
+                         "rotquant: the fused rotate+quantize kernel alone at M=4608 and M=16384")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -122,6 +124,9 @@ def main():
         return
     if args.workload == "gemm-sweep":
         bench_gemm_sweep(args)
+        return
+    if args.workload == "rotquant":
+        bench_rotquant(args)
         return
 
     import torch
@@ -237,7 +242,8 @@ def main():
         copy_cal = {"bytes_read": 1 << 30, "bytes_written": 1 << 30}
         del a, b
 
-    cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
+    cpu = cpu_baseline_torch(args.cpu_seconds) if args.cpu_seconds > 0 else None
+    cpu_c = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
 
     line = {
         "metric": METRIC if args.path != "w8a8" else METRIC.replace("W4A4", "W8A8"),
@@ -250,7 +256,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
+        # the path's arithmetic: int4 codes (int8 codes for the W8A8 tier) with exact
+        # integer accumulation; the products run on BF6 / int8 matrix cores
+        "dtype": "int8" if args.path == "w8a8" else "int4",
         "data": "synthetic",
         "config": {
             "workload": "Flux-class DiT block W4A4 ConvRot linears (qkv 3072->9216, proj 3072->3072, "
@@ -270,9 +278,9 @@ def main():
             "traffic": gemm_traffic_bytes() if args.path == "bf6" else None,
         },
         "rotate_quant": {
-            "kernel": {"bf6": "rotquant_row_kernel<bf16,256,1 pass,B6T out> (3 waves per row)",
-                       "int8": "rotquant_row_kernel<bf16,256,1 pass,packed int4 out> (3 waves per row)",
-                       "w8a8": "rotquant_row_kernel<bf16,256,1 pass,I8T out> (3 waves per row)"}[args.path],
+            "kernel": {"bf6": "rotquant_row_kernel<bf16,256,3 passes,B6T out> (one wave per row)",
+                       "int8": "rotquant_row_kernel<bf16,256,3 passes,packed int4 out> (one wave per row)",
+                       "w8a8": "rotquant_row_kernel<bf16,256,3 passes,I8T out> (one wave per row)"}[args.path],
             "bound": "hbm",
             "GBps_at_M4608_K3072": round(metric_rq_gbs, 1),
             "frac_at_M4608_K3072": round(metric_rq_gbs / PEAK_HBM_GBS, 4),
@@ -284,11 +292,76 @@ def main():
         "gemm_pct_int8_peak": round(100 * gemm_tops / PEAK_INT8_TOPS, 2),
         "detail": detail,
         "cpu_baseline": cpu,
+        "cpu_baseline_c_oracle": cpu_c,
         "host_wall_s": round(wall, 3),
         "ms_per_step_with_kernel_events": round(ms_step_events, 4),
     }
     if copy_cal:
         line["copy_calibration"] = copy_cal
+    print(json.dumps(line), flush=True)
+
+
+RQ_SHAPES = ((4608, 3072), (4608, 12288), (16384, 3072), (16384, 12288))
+
+
+def bench_rotquant(args):
+    """The fused rotate + int4 quantize kernel alone, bf16 [M, K] in, at the
+    block's M=4608 and the standalone M=16384 shapes: x ~ N(0,1) with 1% of
+    channels replaced by Student-t(nu=3) draws at M=16384 (x20 outliers at
+    M=4608), seed 0.  Both outputs: the packed int4 of the reference's C-ABI
+    (ck_convrot_quant_int4) and the B6T operand of the product path.  Several
+    input buffers in rotation (over 600 MB, beyond the 256 MB Infinity Cache);
+    per launch, HIP events on the launch stream, median over --steps.  GB/s =
+    algorithmic bytes (2 B read + 0.5 B written per element + 4 B per row)
+    over time."""
+    import torch
+    from inputs import outlier_activations
+    importlib.import_module("comfyui-int4-convrot-rdna4_amd")
+    native = importlib.import_module("comfyui-int4-convrot-rdna4_amd._int4.native")
+    if not native.is_available():
+        raise SystemExit("libconvrot_gfx950.so is not loadable on a gfx950 device; nothing to measure")
+    lib = native.load_library()
+    stream = torch.cuda.current_stream()
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+    vp = ctypes.c_void_p
+    detail = {}
+    for M, K in RQ_SHAPES:
+        nbuf = max(2, (600 << 20) // (M * K * 2) + 1)
+        base = outlier_activations(M, K, seed=0, student_t=(M == 16384))
+        xs = [base.roll(i, 0).contiguous().cuda() for i in range(nbuf)]
+        q = torch.empty((M, K // 2), dtype=torch.int8, device="cuda")
+        a6 = torch.empty((native.bf6_rows(M), K // 4 * 3), dtype=torch.uint8, device="cuda")
+        s = torch.empty((M,), dtype=torch.float32, device="cuda")
+        for out, fn, dst in (("packed", lib.ck_convrot_quant_int4, q), ("b6t", lib.cr_convrot_quant_bf6, a6)):
+            def launch(b):
+                rc = fn(vp(xs[b % nbuf].data_ptr()), 1, vp(dst.data_ptr()), vp(s.data_ptr()), M, K, G, sptr)
+                if rc != 0:
+                    raise RuntimeError(f"rotate+quant launch failed rc={rc}")
+            for b in range(args.warmup):
+                launch(b)
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+            torch.cuda.synchronize()
+            ev[0].record(stream)
+            for b in range(args.steps):
+                launch(b)
+                ev[b + 1].record(stream)
+            torch.cuda.synchronize()
+            ts = sorted(ev[b].elapsed_time(ev[b + 1]) * 1e-3 for b in range(args.steps))
+            t = ts[len(ts) // 2]
+            alg = rq_bytes(M, K, "int4")
+            detail[f"{M}x{K} {out}"] = {"us": round(t * 1e6, 2), "GBps": round(alg / t / 1e9, 1),
+                                         "frac": round(alg / t / 1e9 / PEAK_HBM_GBS, 4)}
+        del xs
+    head = detail["4608x3072 b6t"]
+    line = {"metric": "rotate-quant GB/s (algorithmic bytes, packed-int4 count) at M=4608,K=3072",
+            "value": head["GBps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(head["us"] / 1e3, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "fused rotate + int4 quantize alone, bf16 [M, K], G=256",
+                       "shapes": [list(x) for x in RQ_SHAPES]},
+            "roofline": {"kernel": "rotquant_row_kernel (B6T out)", "bound": "hbm", "achieved": head["GBps"],
+                         "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": head["frac"], "traffic": None},
+            "detail": detail}
     print(json.dumps(line), flush=True)
 
 
@@ -358,7 +431,9 @@ def bench_gemm_sweep(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
+        # the path's arithmetic: int4 codes (int8 codes for the W8A8 tier) with exact
+        # integer accumulation; the products run on BF6 / int8 matrix cores
+        "dtype": "int8" if args.path == "w8a8" else "int4",
         "data": "synthetic",
         "config": {"workload": "W4A4 GEMM token sweep, bf6 operands, bf16 out + bias: M in %s x (K, N) in %s; codes "
                                "uniform [-8, 7], scales U(0.005, 0.05)" % (list(SWEEP_M), [list(x) for x in SWEEP_KN])},
@@ -511,7 +586,9 @@ def bench_dit(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
+        # the path's arithmetic: int4 codes (int8 codes for the W8A8 tier) with exact
+        # integer accumulation; the products run on BF6 / int8 matrix cores
+        "dtype": "int8" if args.path == "w8a8" else "int4",
         "data": "synthetic",
         "config": {
             "workload": "synthetic double-stream DiT stack through Int4ConvRotOps: 8 blocks, hidden 3072, 24 heads, "
@@ -546,6 +623,58 @@ def _cpu_model() -> str:
     except OSError:
         pass
     return "unknown"
+
+
+def cpu_baseline_torch(target_s: float):
+    """The reference's eager CPU path, restated with the same torch operations
+    (oracle/torch_eager.py; it reproduces the reference eager output bit for
+    bit): for each of the block's four linears, bf16 rotation matmul, bf16
+    rowwise quantize + nibble pack, unpack + bf16 int-code matmul + bf16
+    epilogue, on the first rows of the token batch (weights quantized from fp16
+    beforehand, untimed).  torch's intra-op threads (the box's CPU share); one
+    warm-up, then the median of three repetitions, with per-stage times and
+    rates in the GPU's units (rotate+quant GB/s, GEMM TOPS)."""
+    import torch
+    from oracle import torch_eager as te
+    from inputs import normal_bias, normal_weight, outlier_activations
+
+    layers = []
+    for i, (name, K, N) in enumerate(LINEARS):
+        qw, ws = te.quantize_weight(normal_weight(N, K, seed=11 + i), G)
+        layers.append((K, N, qw, ws, normal_bias(N, seed=21 + i)))
+    threads = torch.get_num_threads()
+
+    x_all = [outlier_activations(M_TOKENS, K, seed=K) for K, *_ in layers]
+
+    def run(rows):
+        stages = {}
+        t0 = time.perf_counter()
+        for x, (K, N, qw, ws, bias) in zip(x_all, layers):
+            te.linear(x[:rows], qw, ws, bias, G, stage_seconds=stages)
+        return time.perf_counter() - t0, stages
+
+    probe = 256
+    run(16)                                             # first-call set-up
+    t, _ = run(probe)                                   # size probe
+    rows = int(max(probe, min(M_TOKENS, probe * (target_s / 4) / max(t, 1e-6))))
+    rows -= rows % 16
+    run(rows)                                           # warm-up at the sample size
+    reps = sorted((run(rows) for _ in range(3)), key=lambda r: r[0])
+    t, stages = reps[1]
+    ops = 2.0 * rows * sum(N * K for _, K, N in LINEARS)
+    rq_b = sum(rq_bytes(rows, K, "int4") for _, K, _ in LINEARS)
+    t_rq = stages["rotate"] + stages["quantize_pack"]
+    cpu = _cpu_model()
+    return {"value": round(ops / t / 1e12, 6), "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"torch restatement of the reference eager path (bf16 rotation matmul, bf16 quantize + "
+                      f"pack, bf16 int-code matmul + epilogue; {threads} torch threads on {cpu}): {rows} of the "
+                      f"{M_TOKENS} rows through the block's four linears; median of 3 repetitions after "
+                      f"warm-up",
+            "seconds": round(t, 3),
+            "stage_seconds": {k: round(v, 3) for k, v in stages.items()},
+            "rotate_quant_GBps": round(rq_b / t_rq / 1e9, 2),
+            "gemm_TOPS": round(ops / stages["gemm_epilogue"] / 1e12, 4),
+            "cpu_model": cpu}
 
 
 def cpu_baseline(target_s: float):

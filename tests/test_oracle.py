@@ -354,3 +354,38 @@ def test_int8_gemm_matches_numpy(oracle):
     acc = oracle.int8_gemm(X, W)
     assert np.array_equal(acc, X.astype(np.int64) @ W.astype(np.int64).T)
     assert acc[0, 0] == 128 * 128 * 4096
+
+
+# ----------------------------------------------------------------------------
+# torch restatement of the eager path (the CPU baseline of bench.py)
+# ----------------------------------------------------------------------------
+
+def test_torch_eager_reproduces_reference_config1(goldens, oracle):
+    """The torch restatement runs the reference's torch operations: on the
+    config-1 linear it gives the reference eager output bit for bit (SHA-256
+    golden), the reference's activation codes and scales, and the fp16 weight
+    codes; its codec inverts the C oracle's on every byte."""
+    from oracle import torch_eager as te
+    x, w, b = config1_x(), config1_weight(), config1_bias()
+    qw, ws = te.quantize_weight(w, 256)
+    assert sha(qw.numpy()) == str(goldens["c1_qw_sha"])
+    assert np.array_equal(ws.numpy(), goldens["c1_wscale"])
+    qx, xs = te.quantize_rows(te.rotate(x, 256))
+    assert np.array_equal(qx.numpy(), goldens["c1_qact"]) and np.array_equal(xs.numpy(), goldens["c1_xscale"])
+    stages = {}
+    y = te.linear(x, qw, ws, b, 256, stage_seconds=stages)
+    assert sha(np_of(y)) == str(goldens["c1_y_sha"])
+    assert set(stages) == {"rotate", "quantize_pack", "gemm_epilogue"}
+    allb = torch.arange(-128, 128, dtype=torch.int32).to(torch.int8).reshape(2, 128)
+    assert np.array_equal(te.unpack(allb).numpy(), oracle.unpack(allb.numpy()))
+    assert torch.equal(te.pack(te.unpack(allb)), allb)
+
+
+def test_torch_eager_hadamard_is_an_involution():
+    from oracle import torch_eager as te
+    for G in (16, 64, 256):
+        h = te.block_hadamard(G, torch.float64)
+        assert torch.equal(h, h.T)
+        assert torch.allclose(h @ h, torch.eye(G, dtype=torch.float64), atol=0, rtol=0)
+    with pytest.raises(ValueError):
+        te.block_hadamard(32, torch.float32)
