@@ -44,6 +44,48 @@ LINEARS = [("qkv", 3072, 9216), ("proj", 3072, 3072), ("mlp_up", 3072, 12288), (
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "w4a4_gemm_bf6_flux_m4608_traffic.md")
 
 
+class HipTimer:
+    """A row of HIP events on one stream, created with hipEventReleaseToDevice
+    (a device-scope release when recorded, not the default system-scope one,
+    so recording an event does not write the L2 back).  Recorded once after
+    every launch, the interval between consecutive events is one launch: the
+    kernel plus its dispatch (about 2 us at M=4608, which back-to-back
+    launches without events hide)."""
+    RELEASE_TO_DEVICE = 0x40000000          # hipEventReleaseToDevice (hip_runtime_api.h)
+
+    def __init__(self, n: int, stream_ptr: int):
+        hip = ctypes.CDLL("libamdhip64.so.7")   # resolves to the HIP runtime torch has loaded
+        hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.hip, self.stream = hip, ctypes.c_void_p(stream_ptr)
+        self.ev = []
+        for _ in range(n):
+            e = ctypes.c_void_p()
+            self._check(hip.hipEventCreateWithFlags(ctypes.byref(e), self.RELEASE_TO_DEVICE), "create")
+            self.ev.append(e)
+
+    @staticmethod
+    def _check(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"hipEvent{what} failed: hipError {rc}")
+
+    def record(self, i: int):
+        self._check(self.hip.hipEventRecord(self.ev[i], self.stream), "Record")
+
+    def seconds(self, i: int, j: int) -> float:
+        """Time from event i to event j (both recorded and complete)."""
+        ms = ctypes.c_float()
+        self._check(self.hip.hipEventElapsedTime(ctypes.byref(ms), self.ev[i], self.ev[j]), "ElapsedTime")
+        return ms.value * 1e-3
+
+    def close(self):
+        for e in self.ev:
+            self.hip.hipEventDestroy(e)
+        self.ev = []
+
+
 def gemm_traffic_bytes():
     """HBM bytes per bf6 GEMM launch (mean over the four linears) as measured by
     the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this workload, scaled
@@ -163,13 +205,11 @@ def main():
                           (vp(L.qx.data_ptr()), vp(L.qw.data_ptr()), vp(L.xs.data_ptr()), vp(L.ws.data_ptr()),
                            vp(L.bias.data_ptr()), vp(L.out.data_ptr()), L.M, L.N, L.K, 1, sptr)))
 
-    def step(events=None):
+    def step(timer=None, base=0):
         for j, (_, _, fn, a) in enumerate(calls):
-            if events is not None:
-                events[j][0].record(stream)
             rc = fn(*a)
-            if events is not None:
-                events[j][1].record(stream)
+            if timer is not None:
+                timer.record(base + j + 1)
             if rc != 0:
                 raise RuntimeError(f"launch failed rc={rc}")
 
@@ -192,23 +232,24 @@ def main():
     wall = time.perf_counter() - t0
     ms_step = t_start.elapsed_time(t_end) / args.steps
 
-    # per-launch durations: the same K steps again, each launch bracketed by HIP
-    # events on the launch stream
-    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
-           for _ in calls] for _ in range(args.steps)]
-    e_start = torch.cuda.Event(enable_timing=True)
-    e_end = torch.cuda.Event(enable_timing=True)
+    # per-launch durations: the same K steps again with one HIP event on the
+    # launch stream after every launch (and one before the first), so launch j
+    # is timed from the event before it to the event after it.  Each interval
+    # also holds the ~2 us dispatch of its launch that back-to-back launches
+    # hide, so these durations sit a little above a kernel trace's.
+    nc = len(calls)
+    timer = HipTimer(args.steps * nc + 1, stream.cuda_stream)
     torch.cuda.synchronize()
-    e_start.record(stream)
+    timer.record(0)
     for s in range(args.steps):
-        step(ev[s])
-    e_end.record(stream)
+        step(timer, s * nc)
     torch.cuda.synchronize()
-    ms_step_events = e_start.elapsed_time(e_end) / args.steps
+    ms_step_events = timer.seconds(0, args.steps * nc) * 1e3 / args.steps
     dur = {}
     for s in range(args.steps):
         for j, (kind, i, _, _) in enumerate(calls):
-            dur.setdefault((kind, i), []).append(ev[s][j][0].elapsed_time(ev[s][j][1]) * 1e-3)  # seconds
+            dur.setdefault((kind, i), []).append(timer.seconds(s * nc + j, s * nc + j + 1))
+    timer.close()
     avg = {k: sum(v) / len(v) for k, v in dur.items()}
 
     total_ops = sum(L.ops() for L in lins)
@@ -339,14 +380,15 @@ def bench_rotquant(args):
                     raise RuntimeError(f"rotate+quant launch failed rc={rc}")
             for b in range(args.warmup):
                 launch(b)
-            ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+            timer = HipTimer(args.steps + 1, stream.cuda_stream)
             torch.cuda.synchronize()
-            ev[0].record(stream)
+            timer.record(0)
             for b in range(args.steps):
                 launch(b)
-                ev[b + 1].record(stream)
+                timer.record(b + 1)
             torch.cuda.synchronize()
-            ts = sorted(ev[b].elapsed_time(ev[b + 1]) * 1e-3 for b in range(args.steps))
+            ts = sorted(timer.seconds(b, b + 1) for b in range(args.steps))
+            timer.close()
             t = ts[len(ts) // 2]
             alg = rq_bytes(M, K, "int4")
             detail[f"{M}x{K} {out}"] = {"us": round(t * 1e6, 2), "GBps": round(alg / t / 1e9, 1),
@@ -405,15 +447,15 @@ def bench_gemm_sweep(args):
                     nb, sptr)
             for _ in range(args.warmup):
                 assert lib.cr_int4_convrot_gemm_bf6_splitk(*call) == 0
-            evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                   for _ in range(args.steps)]
+            timer = HipTimer(args.steps + 1, stream.cuda_stream)
             torch.cuda.synchronize()
-            for e0, e1 in evs:
-                e0.record(stream)
+            timer.record(0)
+            for b in range(args.steps):
                 assert lib.cr_int4_convrot_gemm_bf6_splitk(*call) == 0
-                e1.record(stream)
+                timer.record(b + 1)
             torch.cuda.synchronize()
-            us = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in evs)
+            us = sorted(timer.seconds(b, b + 1) * 1e6 for b in range(args.steps))
+            timer.close()
             med = us[len(us) // 2]
             ops = 2.0 * M * N * K
             detail[f"{M}x{K}->{N}"] = {"us": round(med, 2), "TOPS": round(ops / med / 1e6, 1), "nsplit": ns}
