@@ -494,10 +494,10 @@ def bench_dit(args):
     with the Flux 2 skip list and a rank-32 dynamic LoRA on each of its 64
     quantized linears.  One step = one forward.  Reports the forward time, the
     GPU time inside the quantized linears (HIP events around each call), the
-    same linears' kernels replayed back to back through the C-ABI (rotate+quant,
-    LoRA down projection, GEMM with the LoRA epilogue) and the difference: the
-    per-layer cost of the Linear replacement's host path (casts, allocation,
-    launch gaps)."""
+    same linears replayed back to back through the C-ABI's one-call linear
+    (with and without the LoRA: their difference is the LoRA's cost) and the
+    difference between the two: the per-layer cost of the Linear replacement's
+    host path (casts, allocation, launch gaps)."""
     import torch
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import dit_stack as ds
@@ -562,7 +562,10 @@ def bench_dit(args):
             h.remove()
         lin_ms = sum(a.elapsed_time(b) for _, a, b in evs) / n_instr
 
-        # the same linears' kernels, replayed back to back through the C-ABI
+        # the same linears replayed back to back through the C-ABI's one-call
+        # linear (the Linear's own launches: LoRA partial sums, rotate+quant
+        # with the LoRA sum, GEMM with the LoRA epilogue), with and without the
+        # LoRA; one HIP event after every call
         lib = native.load_library()
         sptr = ctypes.c_void_p(stream.cuda_stream)
         vp = ctypes.c_void_p
@@ -573,50 +576,38 @@ def bench_dit(args):
             M, K, N = x.shape[0], m.in_features, m.out_features
             D, U = m._dyn_fused
             R = D.shape[0]
-            a6 = torch.empty((native.bf6_rows(M), K // 4 * 3), dtype=torch.uint8, device="cuda")
-            xs = torch.empty((M,), dtype=torch.float32, device="cuda")
-            t = torch.empty((M, R), dtype=torch.bfloat16, device="cuda")
             out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
             b32 = m.bias.float().contiguous()
-            keep += [x, a6, xs, t, out, b32]
-            calls.append(("rq", lib.cr_convrot_quant_bf6, (vp(x.data_ptr()), 1, vp(a6.data_ptr()),
-                                                           vp(xs.data_ptr()), M, K, m._qgs, sptr)))
-            calls.append(("lora_down", lib.cr_lora_down, (vp(x.data_ptr()), 1, vp(D.data_ptr()), vp(t.data_ptr()),
-                                                          M, K, R, sptr)))
-            # the GEMM as the Linear runs it: k-split when the library chooses one
-            ns = lib.cr_gemm_bf6_choose_nsplit(M, N, K)
-            nb = lib.cr_gemm_bf6_splitk_workspace(M, N, ns)
+            nb = lib.cr_convrot_w4a4_linear_bf6_workspace(M, N, K, R)
             wsp = torch.empty((max(nb, 16),), dtype=torch.uint8, device="cuda")
-            keep.append(wsp)
-            calls.append(("gemm_lora", lib.cr_int4_convrot_gemm_bf6_splitk,
-                          (vp(a6.data_ptr()), vp(m._q6.data_ptr()), vp(xs.data_ptr()), vp(m._qs.data_ptr()),
-                           vp(b32.data_ptr()), vp(t.data_ptr()), vp(U.data_ptr()), R, ctypes.c_float(1.0),
-                           vp(out.data_ptr()), M, N, K, 1, ns, vp(wsp.data_ptr()), nb, sptr)))
-            calls.append(("gemm_plain", lib.cr_int4_convrot_gemm_bf6_splitk,
-                          (vp(a6.data_ptr()), vp(m._q6.data_ptr()), vp(xs.data_ptr()), vp(m._qs.data_ptr()),
-                           vp(b32.data_ptr()), None, None, 0, ctypes.c_float(0.0),
-                           vp(out.data_ptr()), M, N, K, 1, ns, vp(wsp.data_ptr()), nb, sptr)))
+            keep += [x, out, b32, wsp]
+            for kind, r in (("linear_lora", R), ("linear_plain", 0)):
+                calls.append((kind, lib.cr_convrot_w4a4_linear_bf6,
+                              (vp(x.data_ptr()), 1, vp(m._q6.data_ptr()), vp(m._qs.data_ptr()), vp(b32.data_ptr()),
+                               0, vp(D.data_ptr()) if r else None, vp(U.data_ptr()) if r else None, r,
+                               ctypes.c_float(1.0), vp(out.data_ptr()), 1, M, N, K, m._qgs, vp(wsp.data_ptr()), nb,
+                               sptr)))
         kern = {}
         reps = 3
+        timer = HipTimer(len(calls) + 1, stream.cuda_stream)
         for rep in range(reps + 1):
-            pairs = []
-            for kind, fn, a in calls:
-                ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                ea.record(stream)
+            torch.cuda.synchronize()
+            timer.record(0)
+            for c, (kind, fn, a) in enumerate(calls):
                 rc = fn(*a)
-                eb.record(stream)
+                timer.record(c + 1)
                 if rc != 0:
                     raise RuntimeError(f"{kind} launch failed rc={rc}")
-                pairs.append((kind, ea, eb))
             torch.cuda.synchronize()
             if rep > 0:
-                for kind, ea, eb in pairs:
-                    kern[kind] = kern.get(kind, 0.0) + ea.elapsed_time(eb) / reps
+                for c, (kind, _, _) in enumerate(calls):
+                    kern[kind] = kern.get(kind, 0.0) + timer.seconds(c, c + 1) * 1e3 / reps
+        timer.close()
         del keep
 
     work = ds.quantized_work(DIT_IMG, DIT_TXT, depth=DIT_DEPTH)
     work_lora = ds.quantized_work(DIT_IMG, DIT_TXT, depth=DIT_DEPTH, lora_rank=DIT_RANK)
-    kern_ms = kern["rq"] + kern["lora_down"] + kern["gemm_lora"]
+    kern_ms = kern["linear_lora"]
     line = {
         "metric": "DiT stack forward: quantized-linear TOPS inside the forward (8 double blocks, LoRA r32)",
         "value": round(work / (lin_ms * 1e-3) / 1e12, 2),
@@ -647,7 +638,7 @@ def bench_dit(args):
         "kernel_only_linear_ms": round(kern_ms, 3),
         "linear_overhead_ms": round(lin_ms - kern_ms, 3),
         "linear_overhead_us_per_layer": round((lin_ms - kern_ms) * 1e3 / len(qlayers), 2),
-        "lora_cost_ms": round(kern["lora_down"] + kern["gemm_lora"] - kern["gemm_plain"], 3),
+        "lora_cost_ms": round(kern["linear_lora"] - kern["linear_plain"], 3),
         "quantized_TOP_per_forward": round(work / 1e12, 3),
         "quantized_TOP_per_forward_with_lora": round(work_lora / 1e12, 3),
         "kernel_only_TOPS": round(work / (kern_ms * 1e-3) / 1e12, 1),

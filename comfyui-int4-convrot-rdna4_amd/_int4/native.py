@@ -29,7 +29,7 @@ _IN_DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 EPI_F32, EPI_BF16, EPI_BF16_EAGER, EPI_ACC = 0, 1, 2, 3
 
 # cr_abi_version() of the library these signatures describe
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _vp, _i = ctypes.c_void_p, ctypes.c_int
 _SIGNATURES = {
@@ -38,7 +38,8 @@ _SIGNATURES = {
     "ck_int4_convrot_gemm_splitk": ([_vp] * 5 + [_i] * 4 + [_vp], _i),
     "cr_int4_convrot_gemm_ex": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
     "cr_convrot_quant_int4_stochastic": ([_vp, _i, _vp, _vp, _vp, _i, _i, _i, _vp], _i),
-    "cr_lora_down": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
+    "cr_lora_down": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp, ctypes.c_size_t, _vp], _i),
+    "cr_lora_down_workspace": ([_i, _i, _i], ctypes.c_size_t),
     "cr_int4_convrot_gemm_lora": ([_vp] * 7 + [_i, ctypes.c_float, _vp] + [_i] * 4 + [_vp], _i),
     "cr_int4_to_bf6": ([_vp, _vp, _i, _i, _vp], _i),
     "cr_convrot_quant_bf6": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
@@ -280,7 +281,12 @@ def lora_down(x: torch.Tensor, down: torch.Tensor) -> torch.Tensor:
     if K != K2:
         raise ValueError(f"K mismatch: x {tuple(x.shape)} down {tuple(down.shape)}")
     t = torch.empty((M, R), dtype=torch.bfloat16, device=x.device)
-    rc = lib.cr_lora_down(_ptr(x), _IN_DTYPE_CODE[x.dtype], _ptr(down), _ptr(t), M, K, R, _stream(x.device))
+    if M == 0:
+        return t
+    nbytes = lib.cr_lora_down_workspace(M, K, R)        # 0 for an unsplit shape
+    ws = torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=x.device)
+    rc = lib.cr_lora_down(_ptr(x), _IN_DTYPE_CODE[x.dtype], _ptr(down), _ptr(t), M, K, R, _ptr(ws), nbytes,
+                          _stream(x.device))
     if rc != 0:
         raise RuntimeError(f"cr_lora_down failed, hipError={rc}")
     return t

@@ -14,10 +14,12 @@ hipError_t gemm_lora_launch(const int8_t* Xp, const int8_t* Wp, const float* xs,
                             const float* bias, const void* t, const void* U, int R, float scale, void* out,
                             int M, int N, int K, int epi, hipStream_t st);
 hipError_t lora_down_launch(const void* x, int in_dtype, const void* D, void* t, int M, int K, int R,
-                            hipStream_t st);
+                            float* part, hipStream_t st);
+hipError_t lora_part_launch(const void* x, int in_dtype, const void* D, float* part, void* t, int M, int K, int R,
+                            int* splits, hipStream_t st);
 hipError_t int4_to_bf6_launch(const void* src, void* dst, int rows, int K, hipStream_t st);
 hipError_t rotquant_b6_launch(const void* x, int in_dtype, uint8_t* a6, float* s, int M, int K, int G,
-                              hipStream_t st);
+                              hipStream_t st, const LoraSum* ls);
 int rotquant_b6_max_k();
 hipError_t rotquant_i8_launch(const void* x, int in_dtype, int8_t* q, float* s, int M, int K, int G,
                               hipStream_t st);
@@ -95,9 +97,19 @@ API int ck_int4_convrot_gemm_splitk(const void* Xp, const void* Wp, const void* 
 
 static int lora_rank_ok(int R) { return R >= 32 && R <= 128 && R % 32 == 0; }
 
-API int cr_lora_down(const void* x, int in_dtype, const void* D, void* t, int M, int K, int R, void* stream) {
+API size_t cr_lora_down_workspace(int M, int K, int R) {
+    if (M <= 0 || K <= 0 || K % 16 != 0 || !lora_rank_ok(R)) return 0;
+    return convrot::lora_part_bytes(M, K, R);
+}
+
+API int cr_lora_down(const void* x, int in_dtype, const void* D, void* t, int M, int K, int R, void* workspace,
+                     size_t workspace_bytes, void* stream) {
     if ((in_dtype != 1 && in_dtype != 2) || M < 0 || K <= 0 || K % 16 != 0 || !lora_rank_ok(R)) return -1;
-    hipError_t e = convrot::lora_down_launch(x, in_dtype, D, t, M, K, R, reinterpret_cast<hipStream_t>(stream));
+    if (M == 0) return 0;
+    const size_t need = convrot::lora_part_bytes(M, K, R);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return -1;
+    hipError_t e = convrot::lora_down_launch(x, in_dtype, D, t, M, K, R, reinterpret_cast<float*>(workspace),
+                                             reinterpret_cast<hipStream_t>(stream));
     return (int)e;
 }
 
@@ -126,7 +138,7 @@ API int cr_convrot_quant_bf6(const void* x, int in_dtype, void* a6out, void* sca
     if (!quant_args_ok(in_dtype, M, K, G) || K % 128 != 0 || K > convrot::rotquant_b6_max_k()) return -1;
     return (int)convrot::rotquant_b6_launch(x, in_dtype, reinterpret_cast<uint8_t*>(a6out),
                                             reinterpret_cast<float*>(scaleout), M, K, G,
-                                            reinterpret_cast<hipStream_t>(stream));
+                                            reinterpret_cast<hipStream_t>(stream), nullptr);
 }
 
 API int cr_max_quant_bf6_k(void) { return convrot::rotquant_b6_max_k(); }
@@ -232,7 +244,7 @@ API int cr_int8_convrot_gemm_i8t(const void* X, const void* W, const void* xscal
 // epilogue and the LoRA term.  Intermediates live in the caller's workspace.
 // ---------------------------------------------------------------------------
 namespace {
-struct LinPlan { size_t a6, xs, t, part, total; int nsplit; };
+struct LinPlan { size_t a6, xs, t, lpart, part, total; int nsplit; };
 size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 LinPlan lin_plan(int M, int N, int K, int R) {
     LinPlan p{};
@@ -241,7 +253,8 @@ LinPlan lin_plan(int M, int N, int K, int R) {
     p.a6 = 0;
     p.xs = al256(rows * (size_t)K / 4 * 3);
     p.t = p.xs + al256((size_t)M * 4);
-    p.part = p.t + al256((size_t)M * R * 2);
+    p.lpart = p.t + al256((size_t)M * R * 2);
+    p.part = p.lpart + (R > 0 ? al256(convrot::lora_part_bytes(M, K, R)) : 0);
     p.total = p.part + convrot::gemm_bf6_splitk_workspace(M, N, p.nsplit);
     return p;
 }
@@ -268,12 +281,19 @@ static int linear_bf6_run(const void* x, int in_dtype, const void* W6, const voi
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
     float* xs = reinterpret_cast<float*>(ws + p.xs);
-    hipError_t e = convrot::rotquant_b6_launch(x, in_dtype, ws + p.a6, xs, M, K, G, st);
-    if (e != hipSuccess) return (int)e;
+    // LoRA (R > 0): the down projection first, as t itself or (several k
+    // ranges) as partial sums that the rotate+quant kernel adds up row by row
+    convrot::LoraSum ls{};
+    int splits = 1;
     if (R != 0) {
-        e = convrot::lora_down_launch(x, in_dtype, D, ws + p.t, M, K, R, st);
+        float* lpart = reinterpret_cast<float*>(ws + p.lpart);
+        hipError_t e = convrot::lora_part_launch(x, in_dtype, D, lpart, ws + p.t, M, K, R, &splits, st);
         if (e != hipSuccess) return (int)e;
+        ls = convrot::LoraSum{lpart, reinterpret_cast<__bf16*>(ws + p.t), splits, R};
     }
+    hipError_t e = convrot::rotquant_b6_launch(x, in_dtype, ws + p.a6, xs, M, K, G, st,
+                                               splits > 1 ? &ls : nullptr);
+    if (e != hipSuccess) return (int)e;
     return (int)convrot::gemm_bf6_launch(ws + p.a6, W6, xs, reinterpret_cast<const float*>(wscale), bias, bias_dtype,
                                          R ? ws + p.t : nullptr, U, R, scale, out, M, N, K, epilogue, p.nsplit,
                                          ws + p.part, st);
@@ -339,4 +359,4 @@ API int cr_convrot_w4a4_linear_bf6_noalloc(const void* x, int in_dtype, const vo
 
 API int cr_max_quant_k(void) { return convrot::rotquant_max_k(); }
 
-API int cr_abi_version(void) { return 8; }
+API int cr_abi_version(void) { return 9; }

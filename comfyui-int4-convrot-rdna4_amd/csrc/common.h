@@ -37,6 +37,16 @@ inline hipError_t lds_limit_once(std::atomic<bool> (&done)[kMaxDev], int dev, co
     return e;
 }
 
+// The split LoRA down projection (lora.hip): x rows per workgroup, k splits,
+// k per split.  lora_plan is a pure function of the shape.
+struct LoraPlan { int xr, splits, krange; };
+LoraPlan lora_plan(int M, int K, int R);
+size_t lora_part_bytes(int M, int K, int R);
+
+// What the rotate+quant kernel sums for the linear's LoRA side path: t[m, r] =
+// bf16(part[0, m, r] + .. + part[S-1, m, r]) in that order (S <= 8).
+struct LoraSum { const float* part; __bf16* t; int S, R; };
+
 __device__ __forceinline__ float bf16lo_to_f32(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16hi_to_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 

@@ -483,9 +483,13 @@ __device__ __forceinline__ float fmax3(float a, float b, float c) {
     return r;
 }
 
-template <int DT, int G, int P, int OUT>
+// LR: also finish the linear's LoRA down projection for every row (LoraSum):
+// wave 0 loads the row's partials at the start of the row and stores their sum
+// after the row's codes, so the loads' latency hides behind the rotation.
+template <int DT, int G, int P, int OUT, bool LR>
 __global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
-        const void* __restrict__ x, int8_t* __restrict__ qout, float* __restrict__ sout, int M, int K) {
+        const void* __restrict__ x, int8_t* __restrict__ qout, float* __restrict__ sout, int M, int K,
+        LoraSum ls) {
     constexpr int LPG = G / kChunk;
     constexpr bool B6 = OUT == OUT_B6T;
     constexpr bool INT8 = OUT == OUT_I8 || OUT == OUT_I8T;
@@ -533,6 +537,14 @@ __global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
         const int nrow = row + gridDim.x < M ? row + gridDim.x : row;
         Held<DT> hv[P];
         float lmax = 0.0f;
+        float lp[8];                 // LoRA partials of rank column `lane` (LR, wave 0)
+        if constexpr (LR) {
+            if (wv == 0) {
+#pragma unroll
+                for (int s = 0; s < 8; ++s)
+                    lp[s] = (s < ls.S && lane < ls.R) ? ls.part[((size_t)s * M + row) * ls.R + lane] : 0.0f;
+            }
+        }
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             const int c0 = (p * W + wv) * 64;     // wave-uniform
@@ -670,6 +682,23 @@ __global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
                     make_uint2(o[0], o[1]);
             }
         }
+        if constexpr (LR) {
+            // t = bf16(part[0] + .. + part[S-1]), the order of lora_reduce_kernel
+            if (wv == 0) {
+                if (lane < ls.R) {
+                    float v = 0.0f;
+#pragma unroll
+                    for (int s = 0; s < 8; ++s)
+                        if (s < ls.S) v += lp[s];
+                    ls.t[(size_t)row * ls.R + lane] = (__bf16)v;
+                }
+                for (int j = lane + 64; j < ls.R; j += 64) {     // ranks above 64
+                    float v = 0.0f;
+                    for (int s = 0; s < ls.S; ++s) v += ls.part[((size_t)s * M + row) * ls.R + j];
+                    ls.t[(size_t)row * ls.R + j] = (__bf16)v;
+                }
+            }
+        }
     }
     if constexpr (OUT == OUT_I8T) {   // zero codes in the padding rows of the last 256-row tile
         const int mpad = (M + 255) & ~255;
@@ -710,8 +739,9 @@ static int num_cus() {
 // 52.2 us; M = 4608, K = 12288: 2 x 6 51.1 us, 1 x 12 54.0 us.  The grid is the
 // number of workgroups that fit on the chip at once, lowered so that every
 // workgroup walks the same number of rows.
-template <int DT, int G, int OUT>
-static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K, hipStream_t st) {
+template <int DT, int G, int OUT, bool LR = false>
+static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K, hipStream_t st,
+                                const LoraSum& ls = LoraSum{}) {
     if (M <= 0) return hipSuccess;
     const int np = (K / kChunk + 63) / 64;
     int P = np <= kRowMaxWaves ? np : np <= 2 * kRowMaxWaves ? (np % 3 != 0 ? 2 : 3) : (np + 1) / 2;
@@ -721,9 +751,9 @@ static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K
     if (P == 4 || P == 5) P = 6;
     if (W > kRowMaxWaves || P > kRowMaxPass) return hipErrorInvalidValue;
     const size_t lds = (size_t)W * kRowWaveLds + 16 * sizeof(float);
-    void (*kern)(const void*, int8_t*, float*, int, int) =
-        P == 1 ? rotquant_row_kernel<DT, G, 1, OUT> : P == 2 ? rotquant_row_kernel<DT, G, 2, OUT>
-        : P == 3 ? rotquant_row_kernel<DT, G, 3, OUT> : rotquant_row_kernel<DT, G, 6, OUT>;   // 5..6 passes: 6
+    void (*kern)(const void*, int8_t*, float*, int, int, LoraSum) =
+        P == 1 ? rotquant_row_kernel<DT, G, 1, OUT, LR> : P == 2 ? rotquant_row_kernel<DT, G, 2, OUT, LR>
+        : P == 3 ? rotquant_row_kernel<DT, G, 3, OUT, LR> : rotquant_row_kernel<DT, G, 6, OUT, LR>;   // 5..6 passes: 6
     static std::atomic<int> occupancy[kRowMaxPass + 1][kRowMaxWaves + 1];   // workgroups per CU, per shape
     int per_cu = occupancy[P][W].load(std::memory_order_relaxed);
     if (per_cu == 0) {
@@ -740,7 +770,7 @@ static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K
     if (grid > M) grid = M;
     const int rows = (M + grid - 1) / grid;
     grid = (M + rows - 1) / rows;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * W), lds, st, x, q, s, M, K);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * W), lds, st, x, q, s, M, K, ls);
     return hipGetLastError();
 }
 
@@ -818,15 +848,21 @@ hipError_t rotquant_launch(const void* x, int in_dtype, const void* noise, int8_
 int rotquant_max_k() { return 8 * kMaxThreads * kChunk; }
 
 // fused rotate + quantize into the B6T layout (K % 128 == 0, K <= 12288)
+// With `ls` (not null) the kernel also sums the LoRA partials of every row into ls->t.
 hipError_t rotquant_b6_launch(const void* x, int in_dtype, uint8_t* a6, float* s, int M, int K, int G,
-                              hipStream_t st) {
+                              hipStream_t st, const LoraSum* ls) {
     if (K % 128 != 0 || K > kWaveMaxK || M < 0) return hipErrorInvalidValue;
+    if (ls != nullptr && (ls->S < 1 || ls->S > 8 || ls->R < 1 || ls->part == nullptr || ls->t == nullptr))
+        return hipErrorInvalidValue;
     int8_t* q = reinterpret_cast<int8_t*>(a6);
 #define RB6_G(DT)                                                                                   \
     switch (G) {                                                                                    \
-        case 16: return rq_row_launch<DT, 16, OUT_B6T>(x, q, s, M, K, st);                         \
-        case 64: return rq_row_launch<DT, 64, OUT_B6T>(x, q, s, M, K, st);                         \
-        case 256: return rq_row_launch<DT, 256, OUT_B6T>(x, q, s, M, K, st);                       \
+        case 16: return ls ? rq_row_launch<DT, 16, OUT_B6T, true>(x, q, s, M, K, st, *ls)          \
+                           : rq_row_launch<DT, 16, OUT_B6T>(x, q, s, M, K, st);                    \
+        case 64: return ls ? rq_row_launch<DT, 64, OUT_B6T, true>(x, q, s, M, K, st, *ls)          \
+                           : rq_row_launch<DT, 64, OUT_B6T>(x, q, s, M, K, st);                    \
+        case 256: return ls ? rq_row_launch<DT, 256, OUT_B6T, true>(x, q, s, M, K, st, *ls)        \
+                            : rq_row_launch<DT, 256, OUT_B6T>(x, q, s, M, K, st);                  \
         default: return hipErrorInvalidValue;                                                       \
     }
     switch (in_dtype) {

@@ -105,11 +105,20 @@ int cr_convrot_quant_int4_stochastic(const void* x, int in_dtype, const void* no
  * Down projection of the dynamic-LoRA side path: t = bf16(x @ D^T).
  *   x [M, K] bf16 (in_dtype 1) or f16 (2), D [R, K] bf16, t [M, R] bf16;
  *   R in {32, 64, 96, 128}, K % 16 == 0.
+ * Depending on the shape (never on the device) the projection is split over
+ * k: f32 partial sums go to `workspace` (cr_lora_down_workspace(M, K, R)
+ * bytes; 0 bytes, and workspace may be NULL, for an unsplit shape), then their
+ * sum in split order is rounded once to bf16.  The linear
+ * (cr_convrot_w4a4_linear_bf6) computes the same t bit for bit.
  * Together with cr_int4_convrot_gemm_lora it replaces the per-adapter
  * v.h(x, out) side path of Int4ConvRotOps.Linear._apply_dyn_lora
  * (reference int4_ops.py:181-192), which has no native counterpart there.
  */
-int cr_lora_down(const void* x, int in_dtype, const void* D, void* t, int M, int K, int R, void* stream);
+int cr_lora_down(const void* x, int in_dtype, const void* D, void* t, int M, int K, int R, void* workspace,
+                 size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of cr_lora_down for this shape (0: none needed, or invalid arguments). */
+size_t cr_lora_down_workspace(int M, int K, int R);
 
 /*
  * cr_int4_convrot_gemm_ex (epilogue 0, 1 or 2) plus the LoRA up projection in
@@ -199,7 +208,8 @@ size_t cr_gemm_bf6_splitk_workspace(int M, int N, int nsplit);
  *   out = epilogue(x_rot_quant @ W^T) [+ scale * (x @ D^T) @ U^T]
  * = cr_convrot_quant_bf6 on x, cr_lora_down when R > 0 (x bf16/f16), then the
  * bf6 GEMM (k-split when cr_gemm_bf6_choose_nsplit says so) with epilogue 0..2;
- * the same kernels, so the same bits as those calls made one by one.  W6 is the
+ * the same bits as those calls made one by one (here the LoRA partial sums are
+ * added up by the rotate+quant kernel, in cr_lora_down's order).  W6 is the
  * weight in B6T (cr_int4_to_bf6), wscale f32 [N], bias [N] of bias_dtype (0 f32,
  * 1 bf16, 2 f16: the Linear keeps biases in fp16) or NULL, D
  * [R, K] / U [N, R] bf16 (R = 0: no LoRA).  The activation codes, scales, t and

@@ -91,7 +91,7 @@ def test_load_refuses_other_abi_version(native, monkeypatch):
 
 def test_library_queries_without_gpu(native):
     lib = native.load_library()
-    assert lib.cr_abi_version() == native.ABI_VERSION == 8
+    assert lib.cr_abi_version() == native.ABI_VERSION == 9
     assert lib.cr_max_quant_k() == 32768
     assert lib.cr_max_quant_bf6_k() == 12288
 
@@ -109,10 +109,20 @@ def test_argument_errors_return_minus_one(native):
     assert lib.cr_int4_convrot_gemm_ex(n, n, n, n, n, n, 4, 4, 64, 9, n) == -1
     assert lib.cr_convrot_quant_int4_stochastic(n, 1, n, n, n, 4, 256, 256, n) == -1  # no noise
     f = ctypes.c_float(1.0)
-    assert lib.cr_lora_down(n, 1, n, n, 4, 256, 48, n) == -1        # rank not a multiple of 32
-    assert lib.cr_lora_down(n, 1, n, n, 4, 256, 160, n) == -1       # rank above 128
-    assert lib.cr_lora_down(n, 0, n, n, 4, 256, 32, n) == -1        # f32 input
-    assert lib.cr_lora_down(n, 1, n, n, 4, 40, 32, n) == -1         # K % 16
+    assert lib.cr_lora_down(n, 1, n, n, 4, 256, 48, n, 0, n) == -1        # rank not a multiple of 32
+    assert lib.cr_lora_down(n, 1, n, n, 4, 256, 160, n, 0, n) == -1       # rank above 128
+    assert lib.cr_lora_down(n, 0, n, n, 4, 256, 32, n, 0, n) == -1        # f32 input
+    assert lib.cr_lora_down(n, 1, n, n, 4, 40, 32, n, 0, n) == -1         # K % 16
+    assert lib.cr_lora_down(n, 1, n, n, 4, 512, 32, n, 0, n) == -1        # split shape, no workspace
+    # the split plan, a function of the shape only: 64-row workgroups over 4 k
+    # ranges for the image stream's long rows, 16-row ones over the whole of K
+    # for its short rows (no partials), 16-row ones over 8 ranges for the text stream
+    assert lib.cr_lora_down_workspace(4096, 12288, 32) == 4 * 4096 * 32 * 4
+    assert lib.cr_lora_down_workspace(4096, 3072, 32) == 0
+    assert lib.cr_lora_down_workspace(512, 3072, 32) == 8 * 512 * 32 * 4
+    assert lib.cr_lora_down_workspace(4608, 3072, 64) == 4 * 4608 * 64 * 4
+    assert lib.cr_lora_down_workspace(64, 256, 32) == 0                    # K of one 256-k range: one split
+    assert lib.cr_lora_down_workspace(4, 40, 32) == 0
     assert lib.cr_int4_convrot_gemm_lora(n, n, n, n, n, n, n, 32, f, n, 4, 4, 64, 3, n) == -1  # acc dump
     assert lib.cr_int4_convrot_gemm_lora(n, n, n, n, n, n, n, 32, f, n, 4, 4, 64, 0, n) == -1  # null t/U
     assert lib.cr_int4_convrot_gemm_lora(n, n, n, n, n, n, n, 64, f, n, 4, 4, 48, 0, n) == -1  # K % 32

@@ -139,6 +139,13 @@ def test_linear_with_fused_lora(backend, native, oracle, gpu, M, N, K, G):
     assert np.linalg.norm(lterm) > 0.3 * np.linalg.norm(main)          # the LoRA term matters
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-2
     assert np.linalg.norm((got - main) - lterm) / np.linalg.norm(lterm) < 1e-2
+    # the same bits as the separate calls: the split down projection (whose
+    # partials the linear sums inside its rotate+quant kernel) and the packed
+    # GEMM with the LoRA epilogue
+    tl = native.lora_down(xg, D)
+    qx, xs2 = native.convrot_quant_int4(xg, G)
+    sep = native.int4_convrot_gemm_lora(qx, qw, xs2, ws, bias.float().cuda(), tl, U, 1.0, native.EPI_BF16)
+    assert torch.equal(out.view(torch.int16), sep.view(torch.int16))
 
 
 def test_ops_forward_fused_and_side_path(backend, gpu):
