@@ -14,6 +14,8 @@
 // int4_to_bf6t_kernel from the packed int4 layout or directly by the fused
 // rotate+quant kernel (rotquant.hip).
 
+#include <type_traits>
+
 #include "gemm_common.h"
 
 namespace convrot {
@@ -229,6 +231,27 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
         const uint32_t st = my_lds + (kb % B6_STAGES) * B6_STAGE_BYTES;
         dma16(st + j * 1024, my_src + (size_t)min(kb, nkb - 1) * B6_CHUNK + j * 1024);
     };
+    // Rank-32 LoRA with a bf16 output: the epilogue's t rows m0 .. m0+255 and U
+    // rows n0 .. n0+255 (64 bytes each, 32 KB in all, read once per workgroup
+    // instead of once per wave) are copied into the ring while the last blocks
+    // are multiplied: in phase B of block kb_tu = max(nkb - 2, 0), into that
+    // block's stage, in place of the past-the-end copies that would have gone
+    // there (the last block's phase A skips its own past-the-end copy into the
+    // same stage).  Copy q (0..3) of wave w is 1 KB chunk c = 4 w + q: t rows
+    // m0 + 16 c .. for c < 16, U rows n0 + 16 (c - 16) .. above; rows past M / N
+    // repeat the last one (they feed only outputs that are never stored).
+    constexpr bool LSTAGE = !SPLIT && LR == 1 && (EPI == EPI_BF16 || EPI == EPI_BF16_EAGER);
+    const int kb_tu = nkb >= 2 ? nkb - 2 : 0;
+    auto dma_tu = [&](uint32_t st, int q) __attribute__((always_inline)) {
+        const int c = wave_u * 4 + q;                            // wave-uniform
+        const bool is_t = c < 16;
+        const int r0 = is_t ? m0 + c * 16 : n0 + (c - 16) * 16;   // may lie past M / N (edge tiles)
+        const int last = (is_t ? M : N) - 1;
+        // byte offset from the start of t / U: the lane's row, clamped into the
+        // matrix (0 <= row <= last, so the copy never leaves it)
+        const uint32_t voff = (uint32_t)min(r0 + (lane >> 2), last) * 64 + (lane & 3) * 16;
+        dma16_sv((uint32_t)(uintptr_t)lds6 + st + c * 1024, is_t ? lora.t : lora.U, voff);
+    };
 
     // Hand-scheduled pipeline, two phases per 128-k block kb, three stages.  Phase
     // A: the 8 MFMAs of k step 0 (fragments read in the previous phase B), the
@@ -254,13 +277,19 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
 #pragma unroll
     for (int r = 0; r < 9; ++r) read_one(0, 0, r, F0);
     uint32_t st_cur = 0;                                      // stage of block kb
-    for (int kb = 0; kb < nkb; ++kb) {
+    // One 128-k block.  MODE 0: the copies described above; MODE 1 (block
+    // kb_tu, LSTAGE): phase B copies t / U instead of block kb+3's first half;
+    // MODE 2 (the last block, LSTAGE, nkb >= 2): phase A copies nothing.  The
+    // LSTAGE blocks run as separate loop bodies, so the common one carries no
+    // extra branches or registers.
+    auto block = [&](int kb, auto mode_c) __attribute__((always_inline)) {
+        constexpr int MODE = decltype(mode_c)::value;
         const uint32_t st_nxt = st_cur == (B6_STAGES - 1) * B6_STAGE_BYTES ? 0u : st_cur + B6_STAGE_BYTES;
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             mfma_one(F0, t);
             __builtin_amdgcn_sched_barrier(0);
-            if (t == 2 || t == 4 || t == 6) dma_one(kb + 2, B6_LOADS / 2 + (t - 2) / 2);
+            if (MODE != 2 && (t == 2 || t == 4 || t == 6)) dma_one(kb + 2, B6_LOADS / 2 + (t - 2) / 2);
             reads_after(t, st_cur, 1, F1);
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -274,11 +303,25 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
         for (int t = 0; t < 8; ++t) {
             mfma_one(F1, t);
             __builtin_amdgcn_sched_barrier(0);
-            if (t == 2 || t == 4 || t == 6) dma_one(kb + 3, (t - 2) / 2);
+            if (t == 2 || t == 4 || t == 6) {
+                if (MODE == 1) {
+                    dma_tu(st_cur, t == 2 ? 0 : t == 4 ? 1 : 2);
+                    if (t == 6) dma_tu(st_cur, 3);
+                } else {
+                    dma_one(kb + 3, (t - 2) / 2);
+                }
+            }
             reads_after(t, st_nxt, 0, F0);
             __builtin_amdgcn_sched_barrier(0);
         }
         st_cur = st_nxt;
+    };
+    if constexpr (LSTAGE) {
+        for (int kb = 0; kb < kb_tu; ++kb) block(kb, std::integral_constant<int, 0>{});
+        block(kb_tu, std::integral_constant<int, 1>{});
+        if (nkb >= 2) block(nkb - 1, std::integral_constant<int, 2>{});
+    } else {
+        for (int kb = 0; kb < nkb; ++kb) block(kb, std::integral_constant<int, 0>{});
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));                 // the copies past the end have landed
 
@@ -297,9 +340,19 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
     // keep the epilogue's index arithmetic out of the main loop's registers
     int em0 = m0, en0 = n0, elane = lane;
     asm volatile("" : "+s"(M), "+s"(N), "+v"(em0), "+v"(en0), "+v"(elane));
-    constexpr int SCR = B6_RING_BYTES / (B6_THREADS / 64);
-    epilogue_lds<EPI, 4, 2, LR, SCR>(acc, sc, out, M, N, em0, en0, em0 + wm * 128,
-                                       en0 + wn * 64, elane, lora, lds6 + wave * SCR);
+    if constexpr (LSTAGE) {
+        // t / U sit in the first 32 KB of stage kb_tu % 3; the waves' output
+        // scratch (12 KB each) fills the other two stages
+        const int tu = kb_tu % B6_STAGES;
+        constexpr int SCR = 2 * B6_STAGE_BYTES / (B6_THREADS / 64);
+        uint8_t* scr = lds6 + ((tu + 1 + (wave >> 2)) % B6_STAGES) * B6_STAGE_BYTES + (wave & 3) * SCR;
+        epilogue_lds<EPI, 4, 2, LR, SCR>(acc, sc, out, M, N, em0, en0, em0 + wm * 128, en0 + wn * 64, elane, lora,
+                                         scr, lds6 + tu * B6_STAGE_BYTES);
+    } else {
+        constexpr int SCR = B6_RING_BYTES / (B6_THREADS / 64);
+        epilogue_lds<EPI, 4, 2, LR, SCR>(acc, sc, out, M, N, em0, en0, em0 + wm * 128,
+                                         en0 + wn * 64, elane, lora, lds6 + wave * SCR);
+    }
 }
 
 // Split-K reduce: one 256-lane workgroup per (tile, wave slot) of the main

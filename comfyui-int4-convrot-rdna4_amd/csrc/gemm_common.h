@@ -156,15 +156,21 @@ __device__ __forceinline__ void epilogue_tiles(const AccV (&acc)[FMT][FNT], cons
 // LR selects the LoRA term: 0 none; -1 rank la.R read at run time (one
 // dependent t / U load pair per 16 ranks and tile); 1..4 rank 32 * LR known at
 // compile time, loaded in batches of 32 ranks (two t and two U fragments) per
-// tile.  For rank 32 with a bf16 output the U fragments of the wave's columns
-// are loaded once and the t fragments of row tile i + 1 while tile i is
-// finished, so the wave waits for L2 about once in all (more registers than
-// the other cases can spare).  The MFMA sequence (16-rank steps in ascending
-// order) is the same in every mode, so are the results.
+// tile.  For rank 32 with a bf16 output the t fragments of all the wave's row
+// tiles and the U fragments of its columns are loaded together up front, so
+// the wave waits for them once (a row tile's work is too short to hide the
+// next tile's load: fetching t one row tile ahead cost ~3 us per 256 x 256
+// tile).  The MFMA sequence (16-rank steps in ascending order) is the same in
+// every mode, so are the results.
+//
+// tu_lds (rank 32, bf16 output only): the workgroup tile's t rows tile_m0 ..
+// +255 and U rows tile_n0 .. +255 staged in LDS (64 bytes per row, U at
+// +16384), read there instead of from global memory.
 template <int EPI, int FMT, int FNT, int LR, int SCR_BYTES, int ASH = 8, typename AccV>
 __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const float* sc,
                                              void* __restrict__ out, int M, int N, int tile_m0, int tile_n0,
-                                             int row0, int col0, int lane, const LoraArgs& la, uint8_t* scr) {
+                                             int row0, int col0, int lane, const LoraArgs& la, uint8_t* scr,
+                                             const uint8_t* tu_lds = nullptr) {
     constexpr bool LORA = LR != 0;
     constexpr bool PRE = LR == 1 && (EPI == EPI_BF16 || EPI == EPI_BF16_EAGER);
     constexpr int ES = (EPI == EPI_BF16 || EPI == EPI_BF16_EAGER) ? 2 : 4;
@@ -183,36 +189,33 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
     auto load_t2 = [&](int i, int s0, bf16x8_t (&dst)[2]) {
         const int trow = row0 + i * 32 + l32;
 #pragma unroll
-        for (int s = 0; s < 2; ++s)
-            dst[s] = trow < M ? *reinterpret_cast<const bf16x8_t*>(la.t + (size_t)trow * RK + 16 * (s0 + s) + 8 * h)
-                              : (bf16x8_t){0};
+        for (int s = 0; s < 2; ++s) {
+            const int k = 16 * (s0 + s) + 8 * h;
+            if (PRE && tu_lds != nullptr)
+                dst[s] = trow < M ? *reinterpret_cast<const bf16x8_t*>(tu_lds + (trow - tile_m0) * 64 + 2 * k)
+                                  : (bf16x8_t){0};
+            else
+                dst[s] = trow < M ? *reinterpret_cast<const bf16x8_t*>(la.t + (size_t)trow * RK + k) : (bf16x8_t){0};
+        }
     };
     auto load_u2 = [&](int j, int s0, bf16x8_t (&dst)[2]) {
         const int ucol = col0 + j * 32 + l32;
 #pragma unroll
-        for (int s = 0; s < 2; ++s)
-            dst[s] = ucol < N ? *reinterpret_cast<const bf16x8_t*>(la.U + (size_t)ucol * RK + 16 * (s0 + s) + 8 * h)
-                              : (bf16x8_t){0};
+        for (int s = 0; s < 2; ++s) {
+            const int k = 16 * (s0 + s) + 8 * h;
+            if (PRE && tu_lds != nullptr)
+                dst[s] = ucol < N ? *reinterpret_cast<const bf16x8_t*>(tu_lds + 16384 + (ucol - tile_n0) * 64 + 2 * k)
+                                  : (bf16x8_t){0};
+            else
+                dst[s] = ucol < N ? *reinterpret_cast<const bf16x8_t*>(la.U + (size_t)ucol * RK + k) : (bf16x8_t){0};
+        }
     };
-    bf16x8_t uf[PRE ? FNT : 1][2], tfc[2], tfn[2];
+    bf16x8_t uf[PRE ? FNT : 1][2], tall[PRE ? FMT : 1][2];
     if constexpr (PRE) {
-        load_t2(0, 0, tfc);
+#pragma unroll
+        for (int i = 0; i < FMT; ++i) load_t2(i, 0, tall[i]);
 #pragma unroll
         for (int j = 0; j < FNT; ++j) load_u2(j, 0, uf[j]);
-    }
-    // per-lane column scales and biases of the 4 quads of each column tile
-    float wv[FNT][4][4], bvv[FNT][4][4];
-    if constexpr (EPI != EPI_ACC && EPI != EPI_ATOMIC_ACC) {
-#pragma unroll
-        for (int j = 0; j < FNT; ++j)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int c = col0 - tile_n0 + j * 32 + 4 * h + 8 * q;
-                const float4 w4 = *reinterpret_cast<const float4*>(sc + 256 + c);
-                const float4 b4 = *reinterpret_cast<const float4*>(sc + 512 + c);
-                wv[j][q][0] = w4.x; wv[j][q][1] = w4.y; wv[j][q][2] = w4.z; wv[j][q][3] = w4.w;
-                bvv[j][q][0] = b4.x; bvv[j][q][1] = b4.y; bvv[j][q][2] = b4.z; bvv[j][q][3] = b4.w;
-            }
     }
 #pragma unroll
     for (int i0 = 0; i0 < FMT; i0 += PT) {
@@ -220,16 +223,13 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
         for (int ii = 0; ii < PT; ++ii) {
             const int i = i0 + ii;
             const float xsv = sc[row0 - tile_m0 + i * 32 + l32];
-            if constexpr (PRE) {
-                if (i + 1 < FMT) load_t2(i + 1, 0, tfn);
-            }
 #pragma unroll
             for (int j = 0; j < FNT; ++j) {
                 f32x16_t lacc = (f32x16_t){0};
                 if constexpr (PRE) {
 #pragma unroll
                     for (int s = 0; s < 2; ++s)
-                        lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(uf[j][s], tfc[s], lacc, 0, 0, 0);   // transposed
+                        lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(uf[j][s], tall[i][s], lacc, 0, 0, 0);   // transposed
                 } else if constexpr (LR > 0) {
 #pragma unroll
                     for (int c = 0; c < LR; ++c) {                     // 32 ranks per batch of loads
@@ -255,6 +255,16 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     uint8_t* dst = scr + (ii * 32 + l32) * RS + (j * 32 + 8 * q + 4 * h) * ES;
+                    // this quad's column scales and biases, read from the staged
+                    // copy each time (cheaper than holding 32 registers per tile)
+                    float wq[4] = {0.f, 0.f, 0.f, 0.f}, bq[4] = {0.f, 0.f, 0.f, 0.f};
+                    if constexpr (EPI != EPI_ACC && EPI != EPI_ATOMIC_ACC) {
+                        const int c = col0 - tile_n0 + j * 32 + 4 * h + 8 * q;
+                        const float4 w4 = *reinterpret_cast<const float4*>(sc + 256 + c);
+                        const float4 b4 = *reinterpret_cast<const float4*>(sc + 512 + c);
+                        wq[0] = w4.x; wq[1] = w4.y; wq[2] = w4.z; wq[3] = w4.w;
+                        bq[0] = b4.x; bq[1] = b4.y; bq[2] = b4.z; bq[3] = b4.w;
+                    }
                     if constexpr (EPI == EPI_ACC || EPI == EPI_ATOMIC_ACC) {
                         *reinterpret_cast<int4*>(dst) = make_int4(acc_int<ASH>(acc[i][j][4 * q]), acc_int<ASH>(acc[i][j][4 * q + 1]),
                                                                   acc_int<ASH>(acc[i][j][4 * q + 2]), acc_int<ASH>(acc[i][j][4 * q + 3]));
@@ -265,13 +275,13 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
                             const float a = acc_float<ASH>(acc[i][j][4 * q + e]);
                             if constexpr (EPI == EPI_BF16_EAGER) {
                                 float t = bf16r(bf16r(a) * bf16r(xsv));
-                                t = bf16r(t * bf16r(wv[j][q][e]));
-                                t = bf16r(t + bf16r(bvv[j][q][e]));                 // -0 when there is no bias
+                                t = bf16r(t * bf16r(wq[e]));
+                                t = bf16r(t + bf16r(bq[e]));                        // -0 when there is no bias
                                 if constexpr (LORA) t = bf16r(t + bf16r(__fmul_rn(la.scale, lacc[4 * q + e])));
                                 v[e] = t;
                             } else {
-                                float t = __fmul_rn(__fmul_rn(a, xsv), wv[j][q][e]);
-                                t = __fadd_rn(t, bvv[j][q][e]);                     // -0 when there is no bias
+                                float t = __fmul_rn(__fmul_rn(a, xsv), wq[e]);
+                                t = __fadd_rn(t, bq[e]);                            // -0 when there is no bias
                                 if constexpr (LORA) t = __fadd_rn(t, __fmul_rn(la.scale, lacc[4 * q + e]));
                                 v[e] = t;
                             }
@@ -283,10 +293,6 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
                         }
                     }
                 }
-            }
-            if constexpr (PRE) {
-                tfc[0] = tfn[0];
-                tfc[1] = tfn[1];
             }
         }
         wave_sync();
@@ -365,6 +371,16 @@ __device__ __forceinline__ void dma16(uint32_t lds_addr, const void* src) {
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
                  :
                  : "s"(m0v), "v"(src)
+                 : "memory", "m0");
+}
+
+// The same copy with a wave-uniform base address and a per-lane byte offset
+// (the SADDR form: one VGPR per lane instead of a 64-bit address).
+__device__ __forceinline__ void dma16_sv(uint32_t lds_addr, const void* base, uint32_t voff) {
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_addr);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(m0v), "v"(voff), "s"(base)
                  : "memory", "m0");
 }
 

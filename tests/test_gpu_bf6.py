@@ -99,10 +99,14 @@ def test_bf6_epilogues_bitexact(native, oracle, gpu, M, N, K, bias):
     assert np.array_equal(eg.view(np.uint16), oracle.epilogue_eager_bf16(acc, xs, ws, b))
 
 
-@pytest.mark.parametrize("M,N,K,R", [(64, 48, 256, 32), (257, 300, 3072, 96), (4608, 3072, 3072, 128)])
+@pytest.mark.parametrize("M,N,K,R", [(64, 48, 256, 32), (257, 300, 3072, 96), (4608, 3072, 3072, 128),
+                                     (77, 301, 128, 32), (300, 77, 384, 32), (4097, 3000, 3072, 32),
+                                     (513, 9216, 3072, 32)])
 def test_bf6_lora_equals_int8_path(native, gpu, M, N, K, R):
     """Same accumulators, same epilogue, same LoRA MFMA: outputs identical to
-    the int8-MFMA kernel's for every epilogue."""
+    the int8-MFMA kernel's for every epilogue.  Rank 32 with a bf16 output
+    stages t / U in LDS during the last blocks (one 128-k block, two, three;
+    ragged M and N: the staged rows past M / N repeat the last one)."""
     print(f"bf6 lora M={M} N={N} K={K} R={R}", flush=True)
     xp, wp, xs, ws, b = rand_case(M, N, K, M + R)
     rs = np.random.RandomState(R)
