@@ -522,10 +522,11 @@ __global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
 
     // One chunk buffer, loaded one pass ahead: while pass p is rotated, the
     // wave already loads its next live pass of the row, or its first pass of
-    // the workgroup's next row.  Loads are unconditional (a lane past the row
-    // end reads the pass's first chunk, the last row re-reads itself), so the
-    // load overwrites the buffer it was just converted from without a merge of
-    // old and new values.
+    // the workgroup's next row (none after the workgroup's last row).  Lane
+    // loads are unconditional within a wave (a lane past the row end reads the
+    // pass's first chunk), so the load overwrites the buffer it was just
+    // converted from without a merge of old and new values.  The kernel walks
+    // rows row, row + gridDim.x, ..., so any grid up to M works.
     ChunkRegs<DT> buf;
     int row = blockIdx.x;     // < M: the grid never exceeds M
     {
@@ -559,7 +560,9 @@ __global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
                     const bool same = p + 1 < P && n0 < nchunks;
                     const int lr = same ? row : nrow;
                     const int l0 = same ? n0 : wv * 64;
-                    load_regs<DT>(x, (size_t)lr * K + (size_t)(l0 + lane < nchunks ? l0 + lane : l0) * kChunk, buf);
+                    if (same || nrow != row)   // wave-uniform: the workgroup's last row has no next pass to load
+                        load_regs<DT>(x, (size_t)lr * K + (size_t)(l0 + lane < nchunks ? l0 + lane : l0) * kChunk,
+                                      buf);
                 }
                 rotate_chunk<G>(v, tbuf, lane, gl, gfirst);
                 hold_chunk<DT>(v, hv[p], lmax);
@@ -716,19 +719,6 @@ __global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
     }
 }
 
-// Compute units of the current device (256 on MI355X), cached per device.
-static int num_cus() {
-    static std::atomic<int> cus[kMaxDev];
-    int dev = 0;
-    if (current_device(&dev) != hipSuccess) return 256;
-    int n = cus[dev].load(std::memory_order_relaxed);
-    if (n == 0) {
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
-        cus[dev].store(n, std::memory_order_relaxed);
-    }
-    return n;
-}
-
 // Launch shape: a row is np = ceil(K / 1024) passes of 64 lanes; W <= 4 waves
 // of a workgroup share it with P = ceil(np / W) passes each.  Rows of up to 4
 // passes (K <= 4096) go to one wave each (W = 1, P = np): no barrier between
@@ -736,9 +726,8 @@ static int num_cus() {
 // Longer rows: 2 or 3 passes per wave up to np = 8, else 2 waves of 5..6
 // passes.  Measured (HIP events, bf16 -> B6T): M = 4608, K = 3072: 1 wave x 3
 // passes 17.2 us, 3 x 1 18.3 us; M = 16384, K = 3072: 1 x 3 42.5 us, 3 x 1
-// 52.2 us; M = 4608, K = 12288: 2 x 6 51.1 us, 1 x 12 54.0 us.  The grid is the
-// number of workgroups that fit on the chip at once, lowered so that every
-// workgroup walks the same number of rows.
+// 52.2 us; M = 4608, K = 12288: 2 x 6 51.1 us, 1 x 12 54.0 us.  One workgroup
+// per row (below).
 template <int DT, int G, int OUT, bool LR = false>
 static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K, hipStream_t st,
                                 const LoraSum& ls = LoraSum{}) {
@@ -754,22 +743,14 @@ static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K
     void (*kern)(const void*, int8_t*, float*, int, int, LoraSum) =
         P == 1 ? rotquant_row_kernel<DT, G, 1, OUT, LR> : P == 2 ? rotquant_row_kernel<DT, G, 2, OUT, LR>
         : P == 3 ? rotquant_row_kernel<DT, G, 3, OUT, LR> : rotquant_row_kernel<DT, G, 6, OUT, LR>;   // 5..6 passes: 6
-    static std::atomic<int> occupancy[kRowMaxPass + 1][kRowMaxWaves + 1];   // workgroups per CU, per shape
-    int per_cu = occupancy[P][W].load(std::memory_order_relaxed);
-    if (per_cu == 0) {
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64 * W, lds) != hipSuccess || per_cu < 1)
-            per_cu = 1;
-        occupancy[P][W].store(per_cu, std::memory_order_relaxed);
-    }
-    // Single-wave workgroups: as many as the LDS holds per CU (160 KB on gfx950),
-    // even where the occupancy query reports fewer; the surplus queues behind
-    // the resident ones.  Measured at M = 4608, K = 3072: one row per workgroup
-    // 17.2 us, two 19.3 us; at M = 16384: four rows 42.5 us, eight 50.2 us.
-    if (W == 1) per_cu = per_cu > (int)((160u << 10) / lds) ? per_cu : (int)((160u << 10) / lds);
-    int grid = num_cus() * per_cu;
-    if (grid > M) grid = M;
-    const int rows = (M + grid - 1) / grid;
-    grid = (M + rows - 1) / rows;
+    // One row per workgroup: the hardware queues the surplus behind the
+    // resident workgroups, which beat persistent workgroups walking several
+    // rows (A/B on MI355X, HIP events, bf16 -> B6T, 4 interleaved rounds:
+    // 16384 x 3072 38.3-42.5 us against 41.1-45.0 with 4 rows per workgroup;
+    // 4608 x 12288 45.4-51.5 against 48.0-54.3 with 3; 16384 x 12288
+    // 140.9-153.9 against 153.3-201.4 with 11; 4608 x 3072 runs one row per
+    // workgroup either way, 16.8-17.4 us).
+    const int grid = M;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * W), lds, st, x, q, s, M, K, ls);
     return hipGetLastError();
 }
