@@ -315,7 +315,11 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
                     for (int e = 0; e < 4; ++e)
                         if (col + e < N) atomicAdd(reinterpret_cast<int32_t*>(o) + e, (int32_t)w[e]);
                 } else if (vec && col + EPC <= N) {
-                    *reinterpret_cast<uint4*>(o) = d;
+                    // non-temporal: the output is not read again by this kernel, and
+                    // streaming it past the L2 measured 3% faster over the four Flux
+                    // linears at M = 4608 (proj 6%) in an interleaved A/B
+                    typedef unsigned v4u_st __attribute__((ext_vector_type(4)));
+                    __builtin_nontemporal_store((v4u_st){d.x, d.y, d.z, d.w}, reinterpret_cast<v4u_st*>(o));
                 } else {
                     const uint32_t w[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
