@@ -738,6 +738,15 @@ static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K
     int W = (np + P - 1) / P;
     P = (np + W - 1) / W;
     if (P == 4 || P == 5) P = 6;
+    // Few rows (under two waves per SIMD of the 1024 on MI355X): spread each
+    // row over up to 4 waves, so that a row's passes run side by side instead
+    // of one after another.
+    if ((long long)M * W < 2048 && W < kRowMaxWaves && W < np) {
+        W = np < kRowMaxWaves ? np : kRowMaxWaves;
+        P = (np + W - 1) / W;
+        W = (np + P - 1) / P;
+        if (P == 4 || P == 5) P = 6;
+    }
     if (W > kRowMaxWaves || P > kRowMaxPass) return hipErrorInvalidValue;
     const size_t lds = (size_t)W * kRowWaveLds + 16 * sizeof(float);
     void (*kern)(const void*, int8_t*, float*, int, int, LoraSum) =
