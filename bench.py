@@ -465,11 +465,11 @@ def bench_gemm_sweep(args):
             torch.cuda.synchronize()
             gpu_lead(torch, lead)
             timer.record(0)
-            for b in range(args.steps):
+            for r in range(args.steps):
                 assert lib.cr_int4_convrot_gemm_bf6_splitk(*call) == 0
-                timer.record(b + 1)
+                timer.record(r + 1)
             torch.cuda.synchronize()
-            us = sorted(timer.seconds(b, b + 1) * 1e6 for b in range(args.steps))
+            us = sorted(timer.seconds(r, r + 1) * 1e6 for r in range(args.steps))
             timer.close()
             med = us[len(us) // 2]
             ops = 2.0 * M * N * K

@@ -355,6 +355,172 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Small grids: a 128 x 128 tile per 256-lane workgroup of 4 waves (2 x 2 of
+// 64 x 64 = 2 x 2 MFMA 32 x 32 tiles, 8 MFMAs per 128-k block and wave).  With
+// 256 x 256 tiles a grid of few row tiles (M <= 1024 or so) leaves most CUs
+// idle; a quarter tile quadruples the workgroups at 1.5x the operand bytes
+// per MAC.  A stage is the tile's halves of the A and B chunks of one 128-k
+// block: rows h*128 .. h*128+127 of a B6T chunk are its P bytes h*8192 ..
+// +8191 and its Q row pairs 2h, 2h+1 (bytes 16384 + h*4096 .. +4095), copied
+// into LDS as [P 8 KB][Q 4 KB] (12 KB per operand, 24 KB per stage, 6 DMA
+// instructions per wave), three stages: 75 KB of LDS, two workgroups per CU.
+// The fragment offsets of a local row rl are those of the full chunk with
+// the Q part at 8192 (the swizzle depends on row bits 1..4 only).  Same
+// two-phase schedule as the big kernel: per phase 4 MFMAs, each of the first
+// three followed by the next k step's fragment reads in consumption order and
+// by one DMA instruction (phase A: the second half of block kb+2, phase B: the
+// first half of block kb+3).  Same accumulators, same epilogue: the outputs
+// equal the 256 x 256 kernel's bit for bit.
+// ---------------------------------------------------------------------------
+constexpr int B6S_BM = 128, B6S_BN = 128;
+constexpr int B6S_THREADS = 256;
+constexpr int B6S_STAGES = 3;                                  // 4 and 6 measured no faster
+constexpr int B6S_HALF = B6_CHUNK / 2;                         // 12 KB: one operand half chunk
+constexpr int B6S_STAGE_BYTES = 2 * B6S_HALF;                  // 24 KB
+constexpr int B6S_LOADS = B6S_STAGE_BYTES / 16 / B6S_THREADS;  // 6 DMA instructions per lane
+static_assert(B6S_LOADS == 6, "three copies per phase");
+static_assert((B6S_STAGES - 2) * B6S_LOADS + B6S_LOADS / 2 <= 63, "vmcnt range");
+constexpr int B6S_RING_BYTES = B6S_STAGES * B6S_STAGE_BYTES;
+constexpr int B6S_LDS_BYTES = B6S_RING_BYTES + EPI_SCALE_FLOATS * 4;
+
+template <int EPI, int LR>
+__global__ __launch_bounds__(B6S_THREADS) void w4a4_gemm_bf6_small_kernel(
+        const uint8_t* __restrict__ A6, const uint8_t* __restrict__ W6,
+        const float* __restrict__ xs, const float* __restrict__ ws, const void* __restrict__ bias, int bias_dt,
+        void* __restrict__ out, int M, int N, int K, LoraArgs lora, int gm) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds6[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int tiles_m = (M + B6S_BM - 1) / B6S_BM, tiles_n = (N + B6S_BN - 1) / B6S_BN;
+    const int nkb = K / 128;
+    int tm, tn;
+    tile_of_block(blockIdx.x, tiles_m, tiles_n, gm, tm, tn);
+    const int m0 = tm * B6S_BM;
+    const int n0 = tn * B6S_BN;
+
+    float* sc = reinterpret_cast<float*>(lds6 + B6S_RING_BYTES);
+    stage_scales(sc, xs, ws, bias, bias_dt, M, N, m0, n0, tid, B6S_THREADS);   // visible after the first barrier
+
+    // copy j (0..5) of this wave is instruction w*6 + j of the stage's 24: 0..11
+    // the A half (8 P KB, then 4 Q KB), 12..23 the B half
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const uint8_t* a_chunks = A6 + (size_t)(m0 >> 8) * nkb * B6_CHUNK;
+    const uint8_t* b_chunks = W6 + (size_t)(n0 >> 8) * nkb * B6_CHUNK;
+    const int a_half = (m0 >> 7) & 1, b_half = (n0 >> 7) & 1;
+    auto dma_one = [&](int kb, int j) __attribute__((always_inline)) {
+        const int ins = wave_u * B6S_LOADS + j;                    // wave-uniform, 0..23
+        const bool is_a = ins < 12;
+        const int o = is_a ? ins : ins - 12;                       // KB inside the half image
+        const int h = is_a ? a_half : b_half;
+        const int src_off = o < 8 ? h * 8192 + o * 1024 : B6_QOFF + h * 4096 + (o - 8) * 1024;
+        const uint8_t* chunk = (is_a ? a_chunks : b_chunks) + (size_t)min(kb, nkb - 1) * B6_CHUNK;
+        const uint32_t st = (uint32_t)(uintptr_t)lds6 + (kb % B6S_STAGES) * B6S_STAGE_BYTES +
+                            (is_a ? 0 : B6S_HALF) + o * 1024;
+        dma16(st, chunk + src_off + lane * 16);
+    };
+
+    v16f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (v16f){0};
+
+    const int frow = lane & 31;
+    const int fhalf = lane >> 5;
+    // per-lane byte offsets (inside a stage) of this lane's P and Q pieces for the
+    // two k steps; the wave's second A / B row tile sits 2048 bytes further in P
+    uint32_t offPa[2], offQa[2], offPb[2], offQb[2];
+    {
+        const int ra = wm * 64 + frow, rb = wn * 64 + frow;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const int g = 2 * s2 + fhalf;
+            offPa[s2] = b6_p_off(ra, g);
+            offQa[s2] = b6_q_off(ra, g) - B6_QOFF + 8192;
+            offPb[s2] = B6S_HALF + b6_p_off(rb, g);
+            offQb[s2] = B6S_HALF + b6_q_off(rb, g) - B6_QOFF + 8192;
+        }
+    }
+    struct Frags { v4u pa[2], qa, pb[2], qb; };
+    auto read_one = [&](uint32_t st, int s2, int r, Frags& f) __attribute__((always_inline)) {
+        const uint8_t* base = lds6 + st;
+        if (r < 2) f.pa[r] = *reinterpret_cast<const v4u*>(base + offPa[s2] + r * 2048);
+        else if (r == 2) f.qa = *reinterpret_cast<const v4u*>(base + offQa[s2]);
+        else if (r < 5) f.pb[r - 3] = *reinterpret_cast<const v4u*>(base + offPb[s2] + (r - 3) * 2048);
+        else f.qb = *reinterpret_cast<const v4u*>(base + offQb[s2]);
+    };
+    // MFMA t (0..3): A row tile t / 2 against B row tile t % 2
+    auto mfma_one = [&](const Frags& f, int t) __attribute__((always_inline)) {
+        const int i = t >> 1, j = t & 1;
+        const v8i fa = i ? bf6_operand_odd(f.qa, f.pa[1]) : bf6_operand_even(f.pa[0], f.qa);
+        const v8i fb = j ? bf6_operand_odd(f.qb, f.pb[1]) : bf6_operand_even(f.pb[0], f.qb);
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(   // transposed tile
+                fb, fa, acc[i][j], BF6_FMT, BF6_FMT, 0, E8M0_ONE, 0, E8M0_ONE);
+    };
+    // reads issued after MFMA slot t, in the order the next k step consumes them:
+    // pa0 qa | pb0 qb | pb1 pa1
+    auto reads_after = [&](int t, uint32_t st, int s2, Frags& f) __attribute__((always_inline)) {
+        if (t == 0) { read_one(st, s2, 0, f); read_one(st, s2, 2, f); }
+        if (t == 1) { read_one(st, s2, 3, f); read_one(st, s2, 5, f); }
+        if (t == 2) { read_one(st, s2, 4, f); read_one(st, s2, 1, f); }
+    };
+
+    // Ring of NST stages, block b in stage b % NST: blocks 0 .. NST-2 and the
+    // first half of NST-1 in the prologue; at block kb, phase A copies the second
+    // half of block kb+NST-1 (into block kb-1's stage) and phase B the first
+    // half of block kb+NST (into block kb's stage, free after the barrier).
+    constexpr int NST = B6S_STAGES;
+    Frags F0, F1;
+#pragma unroll
+    for (int b = 0; b < NST - 1; ++b)
+#pragma unroll
+        for (int j = 0; j < B6S_LOADS; ++j) dma_one(b, j);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * B6S_LOADS));   // block 0 landed, blocks 1 .. NST-2 in flight
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < B6S_LOADS / 2; ++j) dma_one(NST - 1, j);   // first half; the second in phase A of block 0
+#pragma unroll
+    for (int r = 0; r < 6; ++r) read_one(0, 0, r, F0);
+    uint32_t st_cur = 0;
+    for (int kb = 0; kb < nkb; ++kb) {
+        const uint32_t st_nxt = st_cur == (NST - 1) * B6S_STAGE_BYTES ? 0u : st_cur + B6S_STAGE_BYTES;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            mfma_one(F0, t);
+            __builtin_amdgcn_sched_barrier(0);
+            if (t >= 1) dma_one(kb + NST - 1, B6S_LOADS / 2 + t - 1);
+            reads_after(t, st_cur, 1, F1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // this wave's copies of block kb+1 landed (those of blocks kb+2 .. kb+NST-1
+        // may be in flight) and its reads of block kb done: after the barrier
+        // block kb's stage is free
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * B6S_LOADS) & 0xc07f);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            mfma_one(F1, t);
+            __builtin_amdgcn_sched_barrier(0);
+            if (t >= 1) dma_one(kb + NST, t - 1);
+            reads_after(t, st_nxt, 0, F0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        st_cur = st_nxt;
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));                 // the copies past the end have landed
+    __syncthreads();                                          // every wave is done with the stages
+    int em0 = m0, en0 = n0, elane = lane;
+    asm volatile("" : "+s"(M), "+s"(N), "+v"(em0), "+v"(en0), "+v"(elane));
+    constexpr int SCR = B6S_RING_BYTES / (B6S_THREADS / 64);
+    epilogue_lds<EPI, 2, 2, LR, SCR>(acc, sc, out, M, N, em0, en0, em0 + wm * 64, en0 + wn * 64, elane, lora,
+                                     lds6 + wave * SCR);
+}
+
 // Split-K reduce: one 256-lane workgroup per (tile, wave slot) of the main
 // kernel; its wave v takes the slot's 32-row tile v.  A wave sums the S
 // partials of its 32 x 64 piece in split order (exact: integers below 2^24)
@@ -399,6 +565,8 @@ __global__ __launch_bounds__(64 * B6R_WAVES) void w4a4_bf6_splitk_reduce_kernel(
                                          lane, lora, scr[v]);
 }
 
+bool gemm_bf6_small_tiles(int M, int N, int K);
+
 template <int EPI, int LR>
 static hipError_t launch_bf6(const uint8_t* A6, const uint8_t* W6, const float* xs, const float* ws,
                              const void* bias, int bias_dt, void* out, int M, int N, int K, const LoraArgs& la,
@@ -408,6 +576,17 @@ static hipError_t launch_bf6(const uint8_t* A6, const uint8_t* W6, const float* 
     int dev = 0;
     hipError_t e = current_device(&dev);
     if (e != hipSuccess) return e;
+    if (nsplit <= 1 && gemm_bf6_small_tiles(M, N, K)) {
+        static std::atomic<bool> attr_small[kMaxDev];
+        e = lds_limit_once(attr_small, dev, reinterpret_cast<const void*>(&w4a4_gemm_bf6_small_kernel<EPI, LR>),
+                           B6S_LDS_BYTES);
+        if (e != hipSuccess) return e;
+        const int sm = (M + B6S_BM - 1) / B6S_BM;
+        const int sn = (N + B6S_BN - 1) / B6S_BN;
+        hipLaunchKernelGGL((w4a4_gemm_bf6_small_kernel<EPI, LR>), dim3(sm * sn), dim3(B6S_THREADS), B6S_LDS_BYTES, st,
+                           A6, W6, xs, ws, bias, bias_dt, out, M, N, K, la, tile_group_rows(sm));
+        return hipGetLastError();
+    }
     const int tiles_m = (M + B6_BM - 1) / B6_BM;
     const int ntiles = tiles_m * ((N + B6_BN - 1) / B6_BN);
     if (nsplit <= 1) {
@@ -480,7 +659,20 @@ hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, cons
 // 128-k block plus 2.5 us; a split adds the reduce kernel, 3.1 us plus 0.09 us
 // per (tile, split) partial (256 KB written and read back).  A split must win
 // by 8% to be taken.
+// The 128 x 128 kernel when its grid stays within about two workgroups per CU
+// and rows are short (long rows go faster through the k-split 256 x 256
+// kernel).  Measured against the 256 x 256 kernel with its chosen split (HIP
+// events, bf16 out): 512 x 3072 -> 3072 16.8 / 25.4 us, 1024 x 3072 -> 3072
+// 17.5 / 23.8, 2048 x 3072 -> 3072 23.5 / 26.3, 512 x 3072 -> 12288 22.0 /
+// 24.5, 512 x 3840 -> 15360 26.9 / 28.6; but 1024 x 3072 -> 9216 34.5 / 26.3
+// and 512 x 12288 -> 3072 41.1 / 32.2.
+bool gemm_bf6_small_tiles(int M, int N, int K) {
+    const long long tiles = (long long)((M + B6S_BM - 1) / B6S_BM) * ((N + B6S_BN - 1) / B6S_BN);
+    return tiles <= 512 && K <= 4096;
+}
+
 int gemm_bf6_choose_nsplit(int M, int N, int K) {
+    if (gemm_bf6_small_tiles(M, N, K)) return 1;
     const int tiles = ((M + B6_BM - 1) / B6_BM) * ((N + B6_BN - 1) / B6_BN);
     const int nkb = K / 128;
     auto cost = [&](int s) {
