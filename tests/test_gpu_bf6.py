@@ -101,12 +101,15 @@ def test_bf6_epilogues_bitexact(native, oracle, gpu, M, N, K, bias):
 
 @pytest.mark.parametrize("M,N,K,R", [(64, 48, 256, 32), (257, 300, 3072, 96), (4608, 3072, 3072, 128),
                                      (77, 301, 128, 32), (300, 77, 384, 32), (4097, 3000, 3072, 32),
-                                     (513, 9216, 3072, 32)])
+                                     (513, 9216, 3072, 32), (100, 200, 256, 128), (2049, 4000, 128, 32),
+                                     (2049, 4000, 256, 32), (2300, 3700, 384, 32), (2049, 4000, 384, 64)])
 def test_bf6_lora_equals_int8_path(native, gpu, M, N, K, R):
     """Same accumulators, same epilogue, same LoRA MFMA: outputs identical to
-    the int8-MFMA kernel's for every epilogue.  Rank 32 with a bf16 output
-    stages t / U in LDS during the last blocks (one 128-k block, two, three;
-    ragged M and N: the staged rows past M / N repeat the last one)."""
+    the int8-MFMA kernel's for every epilogue.  Grids of at most 512 128 x 128
+    tiles with K <= 4096 run the quarter-tile kernel, the rest the 256 x 256
+    one; there, rank 32 with a bf16 output stages t / U in LDS during the last
+    blocks (one 128-k block, two, three; ragged M and N: the staged rows past
+    M / N repeat the last one)."""
     print(f"bf6 lora M={M} N={N} K={K} R={R}", flush=True)
     xp, wp, xs, ws, b = rand_case(M, N, K, M + R)
     rs = np.random.RandomState(R)
