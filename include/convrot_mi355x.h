@@ -168,7 +168,9 @@ int cr_convrot_quant_bf6(const void* x, int in_dtype, void* a6out, void* scaleou
 /* Largest K accepted by cr_convrot_quant_bf6. */
 int cr_max_quant_bf6_k(void);
 
-/* cr_int4_convrot_gemm_ex on B6T operands (A6 from M rows, W6 from N rows); epilogue 0..3. */
+/* cr_int4_convrot_gemm_ex on B6T operands (A6 from M rows, W6 from N rows); epilogue 0..3.
+ * Grids of at most 512 128 x 128 output tiles with K <= 4096 run on 128 x 128
+ * tiles, larger ones on 256 x 256 tiles; the outputs are the same bits. */
 int cr_int4_convrot_gemm_bf6(const void* A6, const void* W6, const void* xscale, const void* wscale,
                              const void* bias, void* out, int M, int N, int K, int epilogue, void* stream);
 
@@ -197,7 +199,8 @@ int cr_int4_convrot_gemm_bf6_splitk(const void* A6, const void* W6, const void* 
                                     void* out, int M, int N, int K, int epilogue, int nsplit,
                                     void* workspace, size_t workspace_bytes, void* stream);
 
-/* The library's k-split count for an M x N x K bf6 GEMM (1 = no split). */
+/* The library's k-split count for an M x N x K bf6 GEMM (1 = no split; always
+ * 1 for the grids that run on 128 x 128 tiles). */
 int cr_gemm_bf6_choose_nsplit(int M, int N, int K);
 
 /* Workspace bytes of cr_int4_convrot_gemm_bf6_splitk: nsplit * tiles * 256 KB (0 when nsplit == 1). */
