@@ -124,11 +124,37 @@ def is_available() -> bool:
 
 
 def _ptr(t):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+    # a plain int: the c_void_p argtypes convert it (None is NULL)
+    return t.data_ptr() if t is not None else None
 
 
-def _stream(device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream(device) -> int:
+    """The current HIP stream of ``device`` as an integer handle (the raw
+    query skips building a torch Stream object per call)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if _raw_stream is not None:
+        return _raw_stream(index)
+    return torch.cuda.current_stream(index).cuda_stream
+
+
+# One reusable workspace per (device, stream): calls on a stream run in stream
+# order, so a call may reuse the workspace of the previous call on the same
+# stream; calls on other streams get their own.  It only grows (a replaced
+# buffer goes back to torch's allocator, which hands it out again only in
+# stream order).
+_workspaces: dict = {}
+
+
+def _workspace(device, stream: int, nbytes: int) -> torch.Tensor:
+    key = (device.index, stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
 
 
 def _check_cuda(*ts):
@@ -284,9 +310,9 @@ def lora_down(x: torch.Tensor, down: torch.Tensor) -> torch.Tensor:
     if M == 0:
         return t
     nbytes = lib.cr_lora_down_workspace(M, K, R)        # 0 for an unsplit shape
-    ws = torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=x.device)
-    rc = lib.cr_lora_down(_ptr(x), _IN_DTYPE_CODE[x.dtype], _ptr(down), _ptr(t), M, K, R, _ptr(ws), nbytes,
-                          _stream(x.device))
+    st = _stream(x.device)
+    ws = _workspace(x.device, st, nbytes)
+    rc = lib.cr_lora_down(_ptr(x), _IN_DTYPE_CODE[x.dtype], _ptr(down), _ptr(t), M, K, R, _ptr(ws), nbytes, st)
     if rc != 0:
         raise RuntimeError(f"cr_lora_down failed, hipError={rc}")
     return t
@@ -391,7 +417,7 @@ def choose_nsplit_bf6(M: int, N: int, K: int) -> int:
 
 def _bf6_launch(a6, w6, xs, wsc, b, t, up, R, scale, out, M, N, K, epilogue, nsplit):
     """One bf6 GEMM: unsplit through the plain entry points, split-K through
-    cr_int4_convrot_gemm_bf6_splitk with a workspace from torch's allocator."""
+    cr_int4_convrot_gemm_bf6_splitk with the stream's workspace."""
     lib = load_library()
     if nsplit is None:
         nsplit = lib.cr_gemm_bf6_choose_nsplit(M, N, K) if M > 0 and N > 0 else 1
@@ -408,7 +434,7 @@ def _bf6_launch(a6, w6, xs, wsc, b, t, up, R, scale, out, M, N, K, epilogue, nsp
             name = "cr_int4_convrot_gemm_bf6_lora"
     else:
         nbytes = lib.cr_gemm_bf6_splitk_workspace(M, N, nsplit)
-        ws = torch.empty((nbytes,), dtype=torch.uint8, device=a6.device)
+        ws = _workspace(a6.device, st, nbytes)
         rc = lib.cr_int4_convrot_gemm_bf6_splitk(_ptr(a6), _ptr(w6), _ptr(xs), _ptr(wsc), _ptr(b), _ptr(t),
                                                  _ptr(up), R, ctypes.c_float(scale), _ptr(out), M, N, K, epilogue,
                                                  nsplit, _ptr(ws), nbytes, st)
@@ -591,11 +617,12 @@ def convrot_w4a4_linear_bf6(x2d, w6, w_scale, bias, down, up, scale: float, epil
     out = torch.empty((M, N), dtype=odt, device=x2d.device)
     R = 0 if down is None else down.shape[0]
     nbytes = lib.cr_convrot_w4a4_linear_bf6_workspace(M, N, K, R)
-    ws = torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=x2d.device)
+    st = _stream(x2d.device)
+    ws = _workspace(x2d.device, st, nbytes)
     bdt = 0 if bias is None else _IN_DTYPE_CODE[bias.dtype]
     rc = lib.cr_convrot_w4a4_linear_bf6(_ptr(x2d), _IN_DTYPE_CODE[x2d.dtype], _ptr(w6), _ptr(w_scale), _ptr(bias),
-                                        bdt, _ptr(down), _ptr(up), R, ctypes.c_float(scale), _ptr(out), epilogue,
-                                        M, N, K, convrot_groupsize, _ptr(ws), nbytes, _stream(x2d.device))
+                                        bdt, _ptr(down), _ptr(up), R, scale, _ptr(out), epilogue,
+                                        M, N, K, convrot_groupsize, _ptr(ws), nbytes, st)
     if rc != 0:
         raise RuntimeError(f"cr_convrot_w4a4_linear_bf6 failed, hipError={rc}")
     return out

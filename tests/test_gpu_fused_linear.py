@@ -57,10 +57,19 @@ def test_single_call_vs_oracle(backend, native, oracle, gpu):
     assert np.array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), want)
 
 
+def _lora_pair(N, K, R, seed):
+    g = torch.Generator().manual_seed(seed)
+    D = (torch.randn(R, K, generator=g) * 0.05).to(torch.bfloat16).cuda()
+    U = (torch.randn(N, R, generator=g) * 0.05).to(torch.bfloat16).cuda()
+    return D, U
+
+
 def test_concurrent_host_threads(backend, native, gpu):
     """Six host threads, each on its own stream, call the single-call linear at
-    once (the library's launch helpers share per-device caches across threads):
-    every call returns the bits of the same call made alone."""
+    once (the library's launch helpers share per-device caches across threads,
+    and the Python layer keeps one workspace per stream): every call returns the
+    bits of the same call made alone.  Every other thread adds a rank-32 LoRA,
+    whose split down projection and the split GEMM use the workspace."""
     import threading
     cases = [(4608, 3072, 3072), (512, 3072, 12288), (77, 640, 3840), (300, 1024, 9216), (1, 256, 128),
              (640, 768, 2048)]
@@ -71,8 +80,9 @@ def test_concurrent_host_threads(backend, native, gpu):
         qw, ws = backend.quantize_convrot_w4a4_weight(normal_weight(N, K, seed=50 + i).cuda(), convrot_groupsize=G)
         w6 = backend.prepare_convrot_w4a4_weight_bf6(qw)
         b = normal_bias(N, seed=60 + i).cuda()
-        want = native.convrot_w4a4_linear_bf6(x, w6, ws, b, None, None, 1.0, native.EPI_BF16, G, N)
-        prepared.append((x, w6, ws, b, G, N, want))
+        D, U = _lora_pair(N, K, 32, 70 + i) if i % 2 == 1 else (None, None)
+        want = native.convrot_w4a4_linear_bf6(x, w6, ws, b, D, U, 1.0, native.EPI_BF16, G, N)
+        prepared.append((x, w6, ws, b, G, N, D, U, want))
     torch.cuda.synchronize()
     got = [None] * len(cases)
     errors = []
@@ -80,11 +90,11 @@ def test_concurrent_host_threads(backend, native, gpu):
 
     def run(i):
         try:
-            x, w6, ws, b, G, N, _ = prepared[i]
+            x, w6, ws, b, G, N, D, U, _ = prepared[i]
             s = torch.cuda.Stream()
             start.wait(timeout=60)
             with torch.cuda.stream(s):
-                outs = [native.convrot_w4a4_linear_bf6(x, w6, ws, b, None, None, 1.0, native.EPI_BF16, G, N)
+                outs = [native.convrot_w4a4_linear_bf6(x, w6, ws, b, D, U, 1.0, native.EPI_BF16, G, N)
                         for _ in range(3)]
             s.synchronize()
             got[i] = outs
@@ -100,4 +110,28 @@ def test_concurrent_host_threads(backend, native, gpu):
     for i, outs in enumerate(got):
         assert outs is not None, f"thread {i} did not finish"
         for y in outs:
-            assert torch.equal(y, prepared[i][6]), cases[i]
+            assert torch.equal(y, prepared[i][8]), cases[i]
+
+
+def test_workspace_reuse_in_stream_order(backend, native, gpu):
+    """Linears of different workspace sizes queued back to back on one stream
+    (the workspace grows, then is reused by smaller calls) give the bits of the
+    same calls made one at a time."""
+    cases = [(64, 128, 256, 32), (512, 3072, 12288, 64), (512, 3072, 3072, 32), (4096, 3072, 12288, 32),
+             (77, 640, 3840, 96), (512, 3072, 12288, 64)]
+    prepared = []
+    for i, (M, N, K, R) in enumerate(cases):
+        G = backend.pick_groupsize(K)
+        x = outlier_activations(M, K, seed=80 + i).cuda()
+        qw, ws = backend.quantize_convrot_w4a4_weight(normal_weight(N, K, seed=90 + i).cuda(), convrot_groupsize=G)
+        w6 = backend.prepare_convrot_w4a4_weight_bf6(qw)
+        b = normal_bias(N, seed=100 + i).cuda()
+        D, U = _lora_pair(N, K, R, 110 + i)
+        want = native.convrot_w4a4_linear_bf6(x, w6, ws, b, D, U, 1.0, native.EPI_BF16, G, N)
+        torch.cuda.synchronize()
+        prepared.append((x, w6, ws, b, G, N, D, U, want))
+    outs = [native.convrot_w4a4_linear_bf6(x, w6, ws, b, D, U, 1.0, native.EPI_BF16, G, N)
+            for (x, w6, ws, b, G, N, D, U, _) in prepared]
+    torch.cuda.synchronize()
+    for c, y, p in zip(cases, outs, prepared):
+        assert torch.equal(y, p[8]), c
