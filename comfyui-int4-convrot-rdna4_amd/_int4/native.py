@@ -171,8 +171,19 @@ def _aligned(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+_limits: dict = {}
+
+
+def _limit(name: str) -> int:
+    # constants of the loaded library, queried once
+    v = _limits.get(name)
+    if v is None:
+        v = _limits[name] = int(getattr(load_library(), name)())
+    return v
+
+
 def max_quant_k() -> int:
-    return int(load_library().cr_max_quant_k())
+    return _limit("cr_max_quant_k")
 
 
 def convrot_quant_int4(x: torch.Tensor, convrot_groupsize: int):
@@ -363,7 +374,7 @@ def int4_to_bf6(packed: torch.Tensor) -> torch.Tensor:
 
 
 def max_quant_bf6_k() -> int:
-    return load_library().cr_max_quant_bf6_k()
+    return _limit("cr_max_quant_bf6_k")
 
 
 def convrot_quant_bf6(x: torch.Tensor, convrot_groupsize: int):
