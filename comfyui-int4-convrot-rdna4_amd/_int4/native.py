@@ -144,11 +144,15 @@ def _stream(device) -> int:
 # order, so a call may reuse the workspace of the previous call on the same
 # stream; calls on other streams get their own.  It only grows (a replaced
 # buffer goes back to torch's allocator, which hands it out again only in
-# stream order).
+# stream order).  Calls captured into a HIP graph get a buffer of their own.
 _workspaces: dict = {}
 
 
 def _workspace(device, stream: int, nbytes: int) -> torch.Tensor:
+    if torch.cuda.is_current_stream_capturing():
+        # a graph keeps the address it captured: give it a buffer of its own
+        # (from the graph's pool), never the stream's shared one
+        return torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=device)
     key = (device.index, stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:

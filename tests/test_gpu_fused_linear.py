@@ -135,3 +135,43 @@ def test_workspace_reuse_in_stream_order(backend, native, gpu):
     torch.cuda.synchronize()
     for c, y, p in zip(cases, outs, prepared):
         assert torch.equal(y, p[8]), c
+
+
+@pytest.mark.parametrize("M,N,K,R", [(512, 3072, 3072, 0), (512, 3072, 3072, 32), (512, 3072, 12288, 32),
+                                     (4608, 3072, 3072, 64)])
+def test_linear_replayed_from_hip_graph(backend, native, gpu, M, N, K, R):
+    """The linear captured into a HIP graph (rotate+quant, LoRA down, GEMM with
+    its split and epilogue: kernel nodes only, no memset) and replayed with new
+    inputs copied into the captured buffer gives the eager call's bits on every
+    replay, with eager calls on the same stream between the replays."""
+    print(f"graph linear M={M} N={N} K={K} R={R}", flush=True)
+    G = backend.pick_groupsize(K)
+    qw, ws = backend.quantize_convrot_w4a4_weight(normal_weight(N, K, seed=120).cuda(), convrot_groupsize=G)
+    w6 = backend.prepare_convrot_w4a4_weight_bf6(qw)
+    b = normal_bias(N, seed=121).cuda()
+    lora = _lora_pair(N, K, R, 122) if R else None
+    xs = [outlier_activations(M, K, seed=130 + i).cuda() for i in range(4)]
+
+    def call(x):
+        return backend.convrot_w4a4_linear(x, qw, ws, b, G, lora=lora, qweight_bf6=w6)
+
+    want = [call(x) for x in xs]
+    torch.cuda.synchronize()
+    static_x = xs[0].clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call(static_x)                       # warm-up outside the capture (first-use attributes)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = call(static_x)
+    for rep in range(2):
+        for i, x in enumerate(xs):
+            static_x.copy_(x)
+            graph.replay()
+            eager = call(xs[(i + 1) % len(xs)])   # eager work between replays
+            torch.cuda.synchronize()
+            assert torch.equal(y, want[i]), (rep, i)
+            assert torch.equal(eager, want[(i + 1) % len(xs)]), (rep, i)
