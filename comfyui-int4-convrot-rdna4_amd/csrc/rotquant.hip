@@ -723,21 +723,32 @@ __global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
 // of a workgroup share it with P = ceil(np / W) passes each.  Rows of up to 4
 // passes (K <= 4096) go to one wave each (W = 1, P = np): no barrier between
 // waves, and the per-row tail (absmax, scale) is paid once per np passes.
-// Longer rows: 2 or 3 passes per wave up to np = 8, else 2 waves of 5..6
-// passes.  Measured (HIP events, bf16 -> B6T): M = 4608, K = 3072: 1 wave x 3
-// passes 17.2 us, 3 x 1 18.3 us; M = 16384, K = 3072: 1 x 3 42.5 us, 3 x 1
-// 52.2 us; M = 4608, K = 12288: 2 x 6 51.1 us, 1 x 12 54.0 us.  One workgroup
-// per row (below).
+// Longer rows: 2 or 3 passes per wave up to np = 8, beyond that 3 passes on
+// each of up to 4 waves (the 3-pass kernel holds fewer registers than the
+// 6-pass one: 4 waves per SIMD instead of 3).  Measured (HIP events, bf16 ->
+// B6T): M = 4608, K = 3072: 1 wave x 3 passes 17.2 us, 3 x 1 18.3 us; M =
+// 16384, K = 3072: 1 x 3 42.5 us, 3 x 1 52.2 us; M = 4608, K = 12288: 2 x 6
+// 51.1 us, 1 x 12 54.0 us, and in an interleaved A/B of 4 x 3 against 2 x 6:
+// M = 2048 22.5 / 26.3 us, 4096 39.3 / 42.4, 4608 43.4 / 45.4, 16384 142.1 /
+// 144.1 (K = 9216: 3 x 3 against 2 x 5, 3-8% faster).  One workgroup per row
+// (below).
 template <int DT, int G, int OUT, bool LR = false>
 static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K, hipStream_t st,
                                 const LoraSum& ls = LoraSum{}) {
     if (M <= 0) return hipSuccess;
     const int np = (K / kChunk + 63) / 64;
-    int P = np <= kRowMaxWaves ? np : np <= 2 * kRowMaxWaves ? (np % 3 != 0 ? 2 : 3) : (np + 1) / 2;
-    if (P == 4) P = 6;                    // 4-pass rows: the 6-pass kernel, its last two passes idle
-    int W = (np + P - 1) / P;
-    P = (np + W - 1) / W;
-    if (P == 4 || P == 5) P = 6;
+    int W, P;
+    if (np <= 2 * kRowMaxWaves) {
+        P = np <= kRowMaxWaves ? np : (np % 3 != 0 ? 2 : 3);
+        if (P == 4) P = 6;                // 4-pass rows: the 6-pass kernel, its last two passes idle
+        W = (np + P - 1) / P;
+        P = (np + W - 1) / W;
+        if (P == 4 || P == 5) P = 6;
+    } else {                              // np = 9..12: 3 passes per wave
+        W = kRowMaxWaves;
+        P = (np + W - 1) / W;
+        W = (np + P - 1) / P;
+    }
     // Few rows (under two waves per SIMD of the 1024 on MI355X): spread each
     // row over up to 4 waves, so that a row's passes run side by side instead
     // of one after another.
@@ -764,7 +775,7 @@ static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K
     return hipGetLastError();
 }
 
-constexpr int kWaveMaxK = 12 * 64 * kChunk;   // 12288: 2 waves x 6 passes
+constexpr int kWaveMaxK = 12 * 64 * kChunk;   // 12288: 4 waves x 3 passes
 
 // ---------------------------------------------------------------------------
 // host-side launch
