@@ -71,6 +71,22 @@ def test_bf6_acc_extremes(native, oracle, gpu):
     assert acc[0, 0] == 64 * K and acc[0, 1] == -56 * K
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 256), (2049, 4096, 256), (2048, 4097, 384), (512, 640, 4096),
+                                   (512, 640, 4224), (1025, 4000, 128)])
+def test_bf6_tile_choice_boundaries(native, oracle, gpu, M, N, K):
+    """Shapes on either side of the 128 x 128 / 256 x 256 kernel choice (512
+    quarter tiles; K 4096 / 4224) and of its split choice: the accumulators
+    equal the int8-MFMA kernel's everywhere and the oracle's on sampled rows."""
+    print(f"bf6 boundary M={M} N={N} K={K} nsplit={native.choose_nsplit_bf6(M, N, K)}", flush=True)
+    xp, wp, *_ = rand_case(M, N, K, M + N + K)
+    xg, wg = cu(xp), cu(wp)
+    acc6 = native.int4_gemm_acc_bf6(native.int4_to_bf6(xg), native.int4_to_bf6(wg), M, N)
+    acc8 = native.int4_gemm_acc(xg, wg)
+    assert torch.equal(acc6, acc8)
+    rows = np.concatenate([np.random.RandomState(K).choice(M, 6, replace=False), [0, M - 1]])
+    assert np.array_equal(acc6.cpu().numpy()[rows], oracle.int_gemm(xp[rows], wp))
+
+
 @pytest.mark.parametrize("M,N,K", [(4608, 3072, 3072), (1024, 3072, 12288)])
 def test_bf6_acc_bitexact_large(native, oracle, gpu, M, N, K):
     print(f"bf6 acc large M={M} N={N} K={K}", flush=True)
