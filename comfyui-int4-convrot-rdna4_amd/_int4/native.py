@@ -11,6 +11,7 @@ back to anything else.
 """
 from __future__ import annotations
 
+import collections
 import ctypes
 import os
 import threading
@@ -142,10 +143,14 @@ def _stream(device) -> int:
 
 # One reusable workspace per (device, stream): calls on a stream run in stream
 # order, so a call may reuse the workspace of the previous call on the same
-# stream; calls on other streams get their own.  It only grows (a replaced
-# buffer goes back to torch's allocator, which hands it out again only in
-# stream order).  Calls captured into a HIP graph get a buffer of their own.
-_workspaces: dict = {}
+# stream; calls on other streams get their own.  It only grows.  A dropped
+# buffer (replaced, or evicted when more than _MAX_WORKSPACES streams are in
+# use) goes back to torch's allocator, which allocated it on that stream and
+# hands it out again only in that stream's order.  Calls captured into a HIP
+# graph get a buffer of their own.
+_MAX_WORKSPACES = 16
+_workspaces: "collections.OrderedDict" = collections.OrderedDict()
+_workspaces_lock = threading.Lock()
 
 
 def _workspace(device, stream: int, nbytes: int) -> torch.Tensor:
@@ -154,10 +159,14 @@ def _workspace(device, stream: int, nbytes: int) -> torch.Tensor:
         # (from the graph's pool), never the stream's shared one
         return torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=device)
     key = (device.index, stream)
-    ws = _workspaces.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=device)
-        _workspaces[key] = ws
+    with _workspaces_lock:
+        ws = _workspaces.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=device)
+            _workspaces[key] = ws
+        _workspaces.move_to_end(key)
+        while len(_workspaces) > _MAX_WORKSPACES:
+            _workspaces.popitem(last=False)
     return ws
 
 

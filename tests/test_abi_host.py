@@ -346,3 +346,26 @@ def test_ops_lora_routing_without_quantization(ops_mod):
         Ops.lora_patches, Ops.lora_dynamic, Ops._applied_lora = {}, False, set()
         for k in ("comfy.lora", "comfy.model_management"):
             sys.modules.pop(k, None)
+
+
+def test_workspace_cache_reuses_grows_and_is_bounded(monkeypatch):
+    """The Python layer's per-stream workspace: reused by later calls on the
+    same stream, replaced when a call needs more, one per stream, and at most
+    _MAX_WORKSPACES streams kept (least recently used dropped first)."""
+    import importlib
+    from conftest import PKG_NAME
+    import_pkg()
+    native = importlib.import_module(PKG_NAME + "._int4.native")
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    monkeypatch.setattr(native, "_workspaces", type(native._workspaces)())
+    dev = torch.device("cpu")
+    a = native._workspace(dev, 1, 100)
+    assert native._workspace(dev, 1, 50) is a
+    b = native._workspace(dev, 1, 200)
+    assert b is not a and b.numel() >= 200
+    assert native._workspace(dev, 2, 10) is not b
+    for s in range(3, 3 + native._MAX_WORKSPACES):
+        native._workspace(dev, s, 10)
+    assert len(native._workspaces) == native._MAX_WORKSPACES
+    assert (None, 1) not in native._workspaces and (None, 2) not in native._workspaces
+    assert (None, 2 + native._MAX_WORKSPACES) in native._workspaces
