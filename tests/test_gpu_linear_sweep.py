@@ -54,3 +54,37 @@ def test_linear_sweep_vs_oracle(backend, oracle, gpu, M, N, K, dt, has_bias):
     else:
         want = oracle.epilogue_f32(acc, exs, ews, bias32, out_bf16=False)
         assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def _long_shapes(n=12, seed=2025):
+    rs = np.random.RandomState(seed)
+    out = []
+    for i in range(n):
+        M = int(rs.choice([300, 513, 1025, 2049]))
+        N = int(rs.randint(1, 1500))
+        K = 128 * int(rs.randint(33, 97))        # 4224 .. 12288: the 256 x 256 kernel, split or not
+        out.append((M, N, K, bool(rs.randint(2))))
+    # enough 256 x 256 tiles that the host rule runs them unsplit
+    return out + [(4099, 1301, 4224, True), (3000, 2000, 6144, False), (4097, 3001, 8320, True)]
+
+
+@pytest.mark.parametrize("M,N,K,has_bias", _long_shapes())
+def test_linear_sweep_long_rows_vs_oracle(backend, native, oracle, gpu, M, N, K, has_bias):
+    """Long rows (K > 4096) and up to 2049 tokens: the 256 x 256 kernel with and
+    without its k-split on ragged shapes.  Codes, scales and sampled output rows
+    bit-exact against the oracle."""
+    print(f"linear sweep long M={M} N={N} K={K} bias={has_bias} nsplit={native.choose_nsplit_bf6(M, N, K)}", flush=True)
+    G = backend.pick_groupsize(K)
+    x = outlier_activations(M, K, seed=11 * M + K, dtype=torch.bfloat16)
+    w = normal_weight(N, K, seed=3 * N + K)
+    b = normal_bias(N, seed=N + 1) if has_bias else None
+    qw, ws = backend.quantize_convrot_w4a4_weight(w.cuda(), convrot_groupsize=G)
+    y = backend.convrot_w4a4_linear(x.cuda(), qw, ws, bias=None if b is None else b.cuda(), convrot_groupsize=G)
+    assert y.shape == (M, N) and y.dtype == torch.bfloat16
+    rows = np.concatenate([np.random.RandomState(M + N).choice(M, 12, replace=False), [0, M - 1]])
+    eqx, exs, _ = oracle.rotquant(bf16_bits(x[rows]), oracle.BF16, G)
+    eqw, ews = oracle.quantize_weight(w.view(torch.int16).numpy().view(np.uint16), oracle.F16, G)
+    assert np.array_equal(qw.cpu().numpy(), eqw)
+    acc = oracle.int_gemm(eqx, eqw)
+    want = oracle.epilogue_f32(acc, exs, ews, None if b is None else b.float().numpy(), out_bf16=True)
+    assert np.array_equal(y.cpu()[rows].view(torch.int16).numpy().view(np.uint16), want)
