@@ -1,6 +1,6 @@
 """Seeded sweep of ragged linear shapes through the Linear's forward path
-(convrot_w4a4_linear: fused rotate+quantize, GEMM, dequant epilogue), bf16 and
-f32 activations, with and without bias.  Every bit equals the oracle's: the
+(convrot_w4a4_linear: fused rotate+quantize, GEMM, dequant epilogue), bf16, f16
+and f32 activations, with and without bias, rows of 64 to 12288 elements.  Every bit equals the oracle's: the
 weight quantizer's codes and scales, then rotate+quantize of x, the integer
 GEMM and the f32 epilogue.  K multiples of 128 take the bf6 GEMM, the other
 multiples of 64 the int8-MFMA GEMM (groupsize 256 or 64 as picked from K)."""
@@ -88,3 +88,31 @@ def test_linear_sweep_long_rows_vs_oracle(backend, native, oracle, gpu, M, N, K,
     acc = oracle.int_gemm(eqx, eqw)
     want = oracle.epilogue_f32(acc, exs, ews, None if b is None else b.float().numpy(), out_bf16=True)
     assert np.array_equal(y.cpu()[rows].view(torch.int16).numpy().view(np.uint16), want)
+
+
+F16_SHAPES = [(1, 64, 64, True), (257, 129, 192, False), (33, 200, 256, True), (300, 1000, 3072, False),
+              (513, 777, 4224, True), (2049, 1500, 12288, False), (4099, 1301, 4224, True)]
+
+
+@pytest.mark.parametrize("M,N,K,has_bias", F16_SHAPES)
+def test_linear_f16_activations_vs_oracle(backend, native, oracle, gpu, M, N, K, has_bias):
+    """fp16 activations and an fp16 bias (as the loader keeps it): the output is the
+    f32 epilogue cast to fp16, as the reference's native path returns it.  The
+    int8 GEMM (K = 192), the 128 x 128 kernel and the 256 x 256 kernel split and
+    unsplit; codes, scales and sampled output rows bit-exact against the oracle."""
+    print(f"linear f16 M={M} N={N} K={K} bias={has_bias}", flush=True)
+    G = backend.pick_groupsize(K)
+    x = outlier_activations(M, K, seed=5 * M + K, dtype=torch.float16)
+    w = normal_weight(N, K, seed=N + 2 * K)
+    b = normal_bias(N, seed=N + 3).to(torch.float16) if has_bias else None
+    qw, ws = backend.quantize_convrot_w4a4_weight(w.cuda(), convrot_groupsize=G)
+    y = backend.convrot_w4a4_linear(x.cuda(), qw, ws, bias=None if b is None else b.cuda(), convrot_groupsize=G)
+    assert y.shape == (M, N) and y.dtype == torch.float16
+    rows = np.unique(np.concatenate([np.random.RandomState(M + K).choice(M, min(M, 12), replace=False), [0, M - 1]]))
+    eqx, exs, _ = oracle.rotquant(x[rows].view(torch.int16).numpy().view(np.uint16), oracle.F16, G)
+    eqw, ews = oracle.quantize_weight(w.view(torch.int16).numpy().view(np.uint16), oracle.F16, G)
+    assert np.array_equal(qw.cpu().numpy(), eqw)
+    acc = oracle.int_gemm(eqx, eqw)
+    want = oracle.epilogue_f32(acc, exs, ews, None if b is None else b.float().numpy(), out_bf16=False)
+    got = y.cpu()[torch.from_numpy(rows)].numpy()
+    assert np.array_equal(got.view(np.uint16), want.astype(np.float16).view(np.uint16))
