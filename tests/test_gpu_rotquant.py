@@ -155,3 +155,37 @@ def test_row_split_launch_shapes(native, oracle, gpu, M, K, G):
     assert torch.equal(s8t.view(torch.int32), s8.view(torch.int32))
     assert np.array_equal(decode_b6t(a6.cpu().numpy(), M), unpack_int4(q.cpu().numpy()))
     assert np.array_equal(q8t.cpu().numpy(), i8t_np(q8.cpu().numpy()))
+
+
+def wide_span_rows(M, K, G, seed):
+    """bf16 rows whose convrot groups span far more than the 36 binades inside
+    which every fp64 partial sum of the rotation is exact: N(0,1) values with a
+    random fifth scaled by 2^-e, e uniform in [20, 140] (down to bf16 subnormals
+    and underflow to zero), and in every group one value repeated at a second
+    position, so that half of the group's outputs cancel it exactly after it
+    has been summed with the tiny values."""
+    rs = np.random.RandomState(seed)
+    x = rs.standard_normal((M, K))
+    tiny = rs.rand(M, K) < 0.2
+    x = np.where(tiny, x * np.exp2(-rs.randint(20, 141, size=(M, K)).astype(np.float64)), x)
+    for g in range(K // G):
+        a, b = g * G + rs.choice(G, 2, replace=False)
+        x[:, b] = x[:, a] = rs.choice([-1.0, 1.0], size=M) * 2.0 ** rs.randint(0, 5)
+    return torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("M,K,G", [(64, 256, 256), (96, 3072, 256), (40, 12288, 256), (64, 3072, 64), (32, 1024, 16)])
+def test_wide_span_groups_vs_oracle(native, oracle, gpu, M, K, G):
+    """Codes and scales of wide-span groups (the fp64 rotation rounds there; the
+    oracle's exact one does not) bit-exact against the oracle, through both the
+    packed int4 and the bf6-operand outputs."""
+    from bf6_format import decode_b6t, unpack_int4
+    x = wide_span_rows(M, K, G, seed=M + K + G)
+    bits = host_bits(x)
+    assert (bits & 0x7f80 == 0).any() and (bits & 0x7fff != 0).any()   # subnormals present
+    q, s = gpu_quant(native, x, G)
+    assert_same(oracle, x, G, q, s)
+    if K % 128 == 0:
+        a6, s6 = native.convrot_quant_bf6(x.cuda(), G)
+        assert np.array_equal(s6.cpu().numpy().view(np.uint32), s.view(np.uint32))
+        assert np.array_equal(decode_b6t(a6.cpu().numpy(), M), unpack_int4(q))
