@@ -27,7 +27,10 @@
 //     multiples of its smallest input ulp bounded by G * max|x|, so they are
 //     exact whenever the group's nonzero inputs span at most 53 - 8 - 2*log4(G)
 //     - 1 binades (bf16; 36 for G = 256), which real activations satisfy by a
-//     wide margin.  The exact value is then rounded once to DT.
+//     wide margin.  The exact value is then rounded once to DT.  Wider groups
+//     get fp64-rounded partial sums in the stage order below (restated on the
+//     CPU by tests/fp64_rotation.py); the reference's own float matmul rounds
+//     those groups too, and more.
 //   * The row absmax is reduced through an LDS atomic max; codes go through
 //     an LDS byte buffer so each lane stores 8 contiguous packed bytes.
 //

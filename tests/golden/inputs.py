@@ -190,3 +190,37 @@ def small_linear_case():
     ws = torch.from_numpy(rs.uniform(0.005, 0.05, size=N).astype(np.float32))
     bias = torch.from_numpy((rs.standard_normal(N) * 0.01).astype(np.float32)).to(torch.float16)
     return xp, wp, xs, ws, bias
+
+
+def wide_span_rows(M, K, G, seed, kind):
+    """bf16 rows whose convrot groups span far more than the 36 binades inside
+    which every fp64 partial sum of the rotation is exact.
+      "mixed": N(0,1) values with a random fifth scaled by 2^-e, e uniform in
+        [20, 140] (down to bf16 subnormals and underflow to zero);
+      "pairs": values of 2^-30 .. 2^-90 and, per group, one value of 1 .. 16
+        at two positions, so that half of the group's outputs cancel it after
+        fp64 partial sums have added the small values to it;
+      "ties": even integers of magnitude <= 256, whose rotated sums often fall
+        exactly on a bf16 rounding midpoint, and a tenth of the values
+        replaced by ones of 2^-40 .. 2^-100 that decide those ties."""
+    rs = np.random.RandomState(seed)
+    if kind == "ties":
+        x = 2.0 * rs.randint(-128, 129, size=(M, K))
+        tiny = rs.rand(M, K) < 0.1
+        x = np.where(tiny, rs.standard_normal((M, K)) * np.exp2(-rs.randint(40, 101, size=(M, K)).astype(np.float64)), x)
+        return torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16)
+    if kind == "mixed":
+        x = rs.standard_normal((M, K))
+        tiny = rs.rand(M, K) < 0.2
+        x = np.where(tiny, x * np.exp2(-rs.randint(20, 141, size=(M, K)).astype(np.float64)), x)
+    else:
+        x = rs.standard_normal((M, K)) * np.exp2(-rs.randint(30, 91, size=(M, K)).astype(np.float64))
+    for g in range(K // G):
+        a, b = g * G + rs.choice(G, 2, replace=False)
+        x[:, b] = x[:, a] = rs.choice([-1.0, 1.0], size=M) * 2.0 ** rs.randint(0, 5)
+    return torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16)
+
+
+# (kind, M, K, G) of the wide-span golden vectors
+WIDE_SPAN_CASES = [("mixed", 16, 3072, 256), ("pairs", 16, 3072, 256), ("ties", 16, 3072, 256),
+                   ("ties", 16, 3072, 64), ("ties", 16, 1024, 16), ("mixed", 16, 1024, 16)]
