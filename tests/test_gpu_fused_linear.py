@@ -28,7 +28,8 @@ def test_single_call_equals_steps(backend, native, gpu, M, N, K, bias_dt):
     assert torch.equal(backend.convrot_w4a4_linear(x, qw, ws, bias=b, convrot_groupsize=G, qweight_bf6=w6), y)
 
 
-@pytest.mark.parametrize("M,N,K,R", [(4608, 3072, 3072, 32), (512, 3072, 12288, 64), (33, 513, 1024, 128)])
+@pytest.mark.parametrize("M,N,K,R", [(4608, 3072, 3072, 32), (512, 3072, 12288, 64), (33, 513, 1024, 128),
+                                     (1024, 1024, 256, 32), (2000, 640, 1024, 64), (1100, 768, 2048, 32)])
 def test_single_call_lora_equals_steps(backend, native, gpu, M, N, K, R):
     x = outlier_activations(M, K, seed=M + 6).cuda()
     qw, ws = backend.quantize_convrot_w4a4_weight(normal_weight(N, K, seed=N + 7).cuda())

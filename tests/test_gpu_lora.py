@@ -28,7 +28,10 @@ def rand_bf16(shape, seed, std):
 DOWN_CASES = [(1, 256, 32, torch.bfloat16), (31, 3072, 64, torch.bfloat16), (33, 2080, 96, torch.float16),
               (300, 3072, 128, torch.bfloat16), (4608, 3072, 128, torch.bfloat16), (100, 12288, 32, torch.float16),
               (7, 1040, 32, torch.bfloat16), (17, 528, 64, torch.bfloat16), (4096, 12288, 32, torch.bfloat16),
-              (512, 3072, 32, torch.float16), (16, 16, 96, torch.bfloat16)]
+              (512, 3072, 32, torch.float16), (16, 16, 96, torch.bfloat16),
+              # 128-row workgroups over k ranges of <= 384 (M >= 1024, K <= 3072, R <= 64)
+              (4096, 3072, 32, torch.bfloat16), (1025, 3072, 64, torch.float16), (2000, 1040, 32, torch.bfloat16),
+              (1024, 256, 32, torch.bfloat16), (1500, 3056, 64, torch.bfloat16)]
 
 
 @pytest.mark.parametrize("M,K,R,dt", DOWN_CASES)
