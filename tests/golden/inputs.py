@@ -221,6 +221,41 @@ def wide_span_rows(M, K, G, seed, kind):
     return torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16)
 
 
+def wide_span_rows_typed(M, K, G, seed, kind, dtype):
+    """The wide-span kinds of wide_span_rows for f32 (24-bit significands: fp64
+    partial sums of a group are exact only within a 20-binade span) and f16
+    (every value a multiple of 2^-24 below 2^16, so a group's sums are
+    multiples of 2^-24 below 2^48 and fp64 holds them all exactly: these rows
+    reach the type's whole range, subnormals included).
+      "mixed": N(0,1) (f16: x4) with a fifth of the values scaled down by
+        2^-20 .. 2^-140 (f16: 2^-8 .. 2^-26, subnormals and underflow);
+      "pairs": small values and, per group, one large value at two positions;
+      "ties": integers of up to 24 (f16: 11) bits, whose rotated sums often
+        fall exactly on a rounding midpoint, and a tenth of the values tiny."""
+    rs = np.random.RandomState(seed)
+    f16 = dtype == torch.float16
+    if kind == "ties":
+        hi = 2 ** 10 if f16 else 2 ** 23
+        x = rs.randint(-hi, hi + 1, size=(M, K)).astype(np.float64)
+        lo = (12, 25) if f16 else (30, 120)
+        tiny = rs.rand(M, K) < 0.1
+        x = np.where(tiny, rs.standard_normal((M, K)) * np.exp2(-rs.randint(*lo, size=(M, K)).astype(np.float64)), x)
+        return torch.from_numpy(x).to(dtype)
+    if kind == "mixed":
+        x = rs.standard_normal((M, K)) * (4.0 if f16 else 1.0)
+        lo = (8, 27) if f16 else (20, 141)
+        tiny = rs.rand(M, K) < 0.2
+        x = np.where(tiny, x * np.exp2(-rs.randint(*lo, size=(M, K)).astype(np.float64)), x)
+    else:
+        lo = (10, 25) if f16 else (30, 91)
+        x = rs.standard_normal((M, K)) * np.exp2(-rs.randint(*lo, size=(M, K)).astype(np.float64))
+    big = (2.0 ** 11, 2.0 ** 12) if f16 else (1.0, 16.0)
+    for g in range(K // G):
+        a, b = g * G + rs.choice(G, 2, replace=False)
+        x[:, b] = x[:, a] = rs.choice([-1.0, 1.0], size=M) * rs.choice(big)
+    return torch.from_numpy(x).to(dtype)
+
+
 # (kind, M, K, G) of the wide-span golden vectors
 WIDE_SPAN_CASES = [("mixed", 16, 3072, 256), ("pairs", 16, 3072, 256), ("ties", 16, 3072, 256),
                    ("ties", 16, 3072, 64), ("ties", 16, 1024, 16), ("mixed", 16, 1024, 16)]

@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from inputs import (WIDE_SPAN_CASES, bf16_bits, config1_x, edge_cases, outlier_activations, stochastic_weight_case,
-                    wide_span_rows)
+                    wide_span_rows, wide_span_rows_typed)
 
 pytestmark = pytest.mark.gpu
 
@@ -177,6 +177,31 @@ def test_wide_span_groups_vs_fp64_restatement(native, oracle, gpu, kind, M, K, G
     xr = rotate_fp64_kernel_order(host_bits(x), G)
     eq, es, _ = oracle.quant_rows(xr, DT[torch.bfloat16])
     eq8, es8 = oracle.quant_rows8(xr, DT[torch.bfloat16])
+    q, s = gpu_quant(native, x, G)
+    assert np.array_equal(q, eq) and np.array_equal(s.view(np.uint32), es.view(np.uint32))
+    q8, s8 = native.convrot_quant_int8(x.cuda(), G)
+    assert np.array_equal(q8.cpu().numpy(), eq8) and np.array_equal(s8.cpu().numpy().view(np.uint32), es8.view(np.uint32))
+    if K % 128 == 0:
+        a6, s6 = native.convrot_quant_bf6(x.cuda(), G)
+        assert np.array_equal(s6.cpu().numpy().view(np.uint32), s.view(np.uint32))
+        assert np.array_equal(decode_b6t(a6.cpu().numpy(), M), unpack_int4(q))
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+@pytest.mark.parametrize("kind,M,K,G", [(k, M, K, G) for k in ("mixed", "pairs", "ties")
+                                        for M, K, G in [(64, 3072, 256), (40, 12288, 256), (32, 1024, 16), (48, 3072, 64)]])
+def test_wide_span_f32_f16_vs_fp64_restatement(native, oracle, gpu, dt, kind, M, K, G):
+    """Genuine f32 inputs (24-bit significands; fp64 partial sums round beyond a
+    20-binade span) and f16 inputs over the whole f16 range (always exact in
+    fp64): int4 codes (packed and B6T), int8 codes and row scales equal the eager
+    quantizers applied to the restated fp64 rotation, bit for bit."""
+    from bf6_format import decode_b6t, unpack_int4
+    from fp64_rotation import rotate_fp64_kernel_order
+    print(f"wide span {dt} {kind} M={M} K={K} G={G}", flush=True)
+    x = wide_span_rows_typed(M, K, G, M + K + G, kind, dt)
+    xr = rotate_fp64_kernel_order(host_bits(x), G, DT[dt])
+    eq, es, _ = oracle.quant_rows(xr, DT[dt])
+    eq8, es8 = oracle.quant_rows8(xr, DT[dt])
     q, s = gpu_quant(native, x, G)
     assert np.array_equal(q, eq) and np.array_equal(s.view(np.uint32), es.view(np.uint32))
     q8, s8 = native.convrot_quant_int8(x.cuda(), G)

@@ -14,13 +14,23 @@ import pytest
 import torch
 
 from fp64_rotation import rotate_fp64_kernel_order
-from inputs import WIDE_SPAN_CASES, config1_x, outlier_activations, wide_span_rows
+from inputs import WIDE_SPAN_CASES, config1_x, outlier_activations, wide_span_rows, wide_span_rows_typed
 
-BF16 = 1
+F32, BF16, F16 = 0, 1, 2
+TORCH_DT = {F32: torch.float32, BF16: torch.bfloat16, F16: torch.float16}
 
 
 def bits(t):
     return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def host(t, dt):
+    return t.contiguous().numpy() if dt == F32 else bits(t)
+
+
+def same(a, b):
+    return np.array_equal(a.view(np.uint32 if a.dtype == np.float32 else np.uint16),
+                          b.view(np.uint32 if b.dtype == np.float32 else np.uint16))
 
 
 @pytest.mark.parametrize("G", [16, 64, 256])
@@ -30,6 +40,31 @@ def test_fp64_restatement_equals_exact_rotation_on_narrow_groups(oracle, G):
     for x in xs:
         b = bits(x)
         assert np.array_equal(rotate_fp64_kernel_order(b, G), oracle.rotate(b, BF16, G))
+    # genuine f32 values (24-bit significands) and f16
+    for dt in (F32, F16):
+        x = torch.from_numpy(np.random.RandomState(G).standard_normal((24, 3072)).astype(np.float32)).to(TORCH_DT[dt])
+        b = host(x, dt)
+        assert same(rotate_fp64_kernel_order(b, G, dt), oracle.rotate(b, dt, G))
+
+
+@pytest.mark.parametrize("kind", ["mixed", "pairs", "ties"])
+@pytest.mark.parametrize("G", [16, 64, 256])
+def test_fp64_rotation_exact_for_every_f16_input(oracle, kind, G):
+    # f16 values are multiples of 2^-24 below 2^16: every partial sum of a
+    # group fits 53 bits, so the kernel's fp64 rotation is the exact one even
+    # on rows that span the whole f16 range
+    x = wide_span_rows_typed(32, 3072 if G > 16 else 1024, G, G + 1, kind, torch.float16)
+    b = host(x, F16)
+    assert (((b & 0x7c00) == 0) & ((b & 0x3ff) != 0)).any()     # subnormals
+    assert ((b & 0x7fff) >= 0x6000).any()                        # and values of 512 and more
+    assert same(rotate_fp64_kernel_order(b, G, F16), oracle.rotate(b, F16, G))
+
+
+def test_fp64_restatement_rounds_on_wide_span_f32(oracle):
+    x = wide_span_rows_typed(32, 3072, 256, 3, "pairs", torch.float32)
+    b = host(x, F32)
+    differ = (rotate_fp64_kernel_order(b, 256, F32).view(np.uint32) != oracle.rotate(b, F32, 256).view(np.uint32)).mean()
+    assert differ > 0.1
 
 
 def test_fp64_restatement_rounds_on_wide_span_ties(oracle):
