@@ -27,7 +27,9 @@
 //     multiples of its smallest input ulp bounded by G * max|x|, so they are
 //     exact whenever the group's nonzero inputs span at most 53 - 8 - 2*log4(G)
 //     - 1 binades (bf16; 36 for G = 256), which real activations satisfy by a
-//     wide margin.  The exact value is then rounded once to DT.  Wider groups
+//     wide margin; f16 inputs always (multiples of 2^-24 below 2^16, so every
+//     partial sum is a multiple of 2^-24 below 2^48).  The exact value is then
+//     rounded once to DT.  Wider groups
 //     get fp64-rounded partial sums in the stage order below (restated on the
 //     CPU by tests/fp64_rotation.py); the reference's own float matmul rounds
 //     those groups too, and more.
