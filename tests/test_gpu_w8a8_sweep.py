@@ -53,3 +53,40 @@ def test_w8a8_linear_sweep_vs_oracle(backend, oracle, gpu, M, N, K, dt, has_bias
     else:
         want = oracle.linear_w8a8(x.float().numpy(), oracle.F32, eqw, ews, bias32, G, out_bf16=False)
         assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+W8A8_TYPED = [(300, 700, 3072, torch.float32, True), (2049, 1000, 12288, torch.float16, False),
+              (513, 257, 4096, torch.float32, False), (1025, 640, 1040, torch.float16, True),
+              (33, 100, 9216, torch.float32, True), (4099, 384, 3072, torch.float16, True)]
+
+
+@pytest.mark.parametrize("M,N,K,dt,has_bias", W8A8_TYPED)
+def test_w8a8_linear_f32_f16_long_rows(backend, oracle, gpu, M, N, K, dt, has_bias):
+    """Genuine f32 activations (24-bit significands, not bf16-grid values) and
+    f16 activations, rows of up to 12288: sampled output rows equal the oracle's
+    int8 quantizer, exact int32 GEMM and f32 epilogue applied to the kernel's
+    fp64 rotation restated on the CPU (f16 output: that epilogue cast to f16)."""
+    from fp64_rotation import rotate_fp64_kernel_order
+    print(f"w8a8 linear {dt} M={M} N={N} K={K} bias={has_bias}", flush=True)
+    i8 = importlib.import_module(backend.__name__ + ".int8_eager")
+    G = backend.pick_groupsize(K)
+    code = oracle.F32 if dt == torch.float32 else oracle.F16
+    x = outlier_activations(M, K, seed=M + 2 * K, dtype=dt)
+    w = normal_weight(N, K, seed=N + 3 * K)
+    b = normal_bias(N, seed=N + 2) if has_bias else None
+    qw, ws = i8.quantize_convrot_w8a8_weight(w.cuda(), convrot_groupsize=G)
+    eqw, ews = oracle.quantize_weight8(w.view(torch.int16).numpy().view(np.uint16), oracle.F16, G)
+    assert np.array_equal(qw.cpu().numpy(), eqw)
+    y = backend.convrot_w8a8_linear(x.cuda(), qw, ws, bias=None if b is None else b.cuda(), convrot_groupsize=G)
+    assert y.shape == (M, N) and y.dtype == dt
+    rows = np.unique(np.concatenate([np.random.RandomState(K).choice(M, min(M, 12), replace=False), [0, M - 1]]))
+    xs_host = x[torch.from_numpy(rows)].contiguous()
+    xb = xs_host.numpy() if dt == torch.float32 else xs_host.view(torch.int16).numpy().view(np.uint16)
+    q8, sx = oracle.quant_rows8(rotate_fp64_kernel_order(xb, G, code), code)
+    acc = oracle.int8_gemm(q8, eqw)
+    want = oracle.epilogue_f32(acc, sx, ews, None if b is None else b.float().numpy(), out_bf16=False)
+    got = y.cpu()[torch.from_numpy(rows)].numpy()
+    if dt == torch.float32:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    else:
+        assert np.array_equal(got.view(np.uint16), want.astype(np.float16).view(np.uint16))
