@@ -116,3 +116,28 @@ def test_linear_f16_activations_vs_oracle(backend, native, oracle, gpu, M, N, K,
     want = oracle.epilogue_f32(acc, exs, ews, None if b is None else b.float().numpy(), out_bf16=False)
     got = y.cpu()[torch.from_numpy(rows)].numpy()
     assert np.array_equal(got.view(np.uint16), want.astype(np.float16).view(np.uint16))
+
+
+@pytest.mark.parametrize("M,N,K,has_bias", F16_SHAPES)
+def test_linear_genuine_f32_activations_vs_oracle(backend, native, oracle, gpu, M, N, K, has_bias):
+    """f32 activations with full 24-bit significands (the sweep above keeps f32
+    values on the bf16 grid): f32 output bit-exact on sampled rows against the
+    eager quantizer, the integer GEMM and the f32 epilogue applied to the
+    kernel's fp64 rotation restated on the CPU."""
+    from fp64_rotation import rotate_fp64_kernel_order
+    print(f"linear f32 M={M} N={N} K={K} bias={has_bias}", flush=True)
+    G = backend.pick_groupsize(K)
+    x = outlier_activations(M, K, seed=9 * M + K, dtype=torch.float32)
+    w = normal_weight(N, K, seed=N + 5 * K)
+    b = normal_bias(N, seed=N + 4) if has_bias else None
+    qw, ws = backend.quantize_convrot_w4a4_weight(w.cuda(), convrot_groupsize=G)
+    y = backend.convrot_w4a4_linear(x.cuda(), qw, ws, bias=None if b is None else b.cuda(), convrot_groupsize=G)
+    assert y.shape == (M, N) and y.dtype == torch.float32
+    rows = np.unique(np.concatenate([np.random.RandomState(M + 2 * K).choice(M, min(M, 12), replace=False), [0, M - 1]]))
+    xr = rotate_fp64_kernel_order(x[torch.from_numpy(rows)].contiguous().numpy(), G, oracle.F32)
+    eqx, exs, _ = oracle.quant_rows(xr, oracle.F32)
+    eqw, ews = oracle.quantize_weight(w.view(torch.int16).numpy().view(np.uint16), oracle.F16, G)
+    assert np.array_equal(qw.cpu().numpy(), eqw)
+    acc = oracle.int_gemm(eqx, eqw)
+    want = oracle.epilogue_f32(acc, exs, ews, None if b is None else b.float().numpy(), out_bf16=False)
+    assert np.array_equal(y.cpu()[torch.from_numpy(rows)].numpy().view(np.uint32), want.view(np.uint32))
