@@ -504,10 +504,12 @@ __global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
     // the row; a wave's LDS operations complete in order).  Codes: bytes (64
     // chunks x 16) for the integer outputs; for B6T the rounded codes as bf16,
     // chunk ch at (ch / 16) * 544 + (ch % 16) * 32 bytes (the pad spreads the
-    // four 16-lane groups over the banks).  After the W wave buffers: the
+    // four 16-lane groups over the banks), one region per pass parity so that
+    // two passes are converted together.  After the W wave buffers: the
     // per-wave row absmax, 8 slots per row parity (slots W..7 hold zeros).
     constexpr int kB6Group = 544;
-    static_assert(kRowWaveLds >= (B6 ? 4 * kB6Group : 64 * 16), "code buffer");
+    constexpr int kB6Region = 4 * kB6Group;
+    static_assert(kRowWaveLds >= (B6 ? 2 * kB6Region : 64 * 16), "code buffer");
     extern __shared__ __attribute__((aligned(16))) double rq_lds[];
 
     const int W = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
@@ -516,8 +518,8 @@ __global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
     double* tbuf = rq_lds + wv * (64 * kPad);
     uint8_t* cb = reinterpret_cast<uint8_t*>(tbuf);
     float* red = reinterpret_cast<float*>(rq_lds + W * (64 * kPad));
-    auto b6_slot = [&](int ch, int pos) {
-        return reinterpret_cast<uint16_t*>(cb + (ch >> 4) * kB6Group + (ch & 15) * 32) + pos;
+    auto b6_slot = [&](int ch, int pos, int region) {
+        return reinterpret_cast<uint16_t*>(cb + region * kB6Region + (ch >> 4) * kB6Group + (ch & 15) * 32) + pos;
     };
     const int nchunks = K / kChunk;
     const int gl = lane % LPG;
@@ -639,25 +641,44 @@ __global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
                     // rint_even(z) as a float, kept as its bf16 bits (exact: an integer of
                     // magnitude <= 7; a zero code may carry the sign of z)
                     const float q0 = __builtin_rintf(z0), q1 = __builtin_rintf(z1);
-                    *b6_slot(gfirst + e0 / kChunk, e0 % kChunk) = (uint16_t)(__float_as_uint(q0) >> 16);
-                    *b6_slot(gfirst + e1 / kChunk, e1 % kChunk) = (uint16_t)(__float_as_uint(q1) >> 16);
+                    *b6_slot(gfirst + e0 / kChunk, e0 % kChunk, p & 1) = (uint16_t)(__float_as_uint(q0) >> 16);
+                    *b6_slot(gfirst + e1 / kChunk, e1 % kChunk, p & 1) = (uint16_t)(__float_as_uint(q1) >> 16);
                 } else {
                     // low byte of the float bits of z + 1.5*2^23 is rint_even(z) (two's complement)
                     cb[(gfirst + e0 / kChunk) * 16 + (e0 % kChunk)] = (uint8_t)__float_as_uint(z0 + kMagic);
                     cb[(gfirst + e1 / kChunk) * 16 + (e1 % kChunk)] = (uint8_t)__float_as_uint(z1 + kMagic);
                 }
             }
-            wave_sync();
-            uint4 w = {}, gq[4];        // gq: filled and used on even lanes only (B6T)
             if constexpr (B6) {
-                // the even lane of a pair reads the pair's 32 codes (64 bytes)
-                if ((lane & 1) == 0) {
+                // The 32 codes of one MFMA group are two consecutive chunks of a pass.
+                // After every odd pass, and after the wave's last pass, lane L takes
+                // group L % 32 of pass (p & ~1) + L / 32: one 32-wide BF6 conversion
+                // per two passes, on every lane (lanes of a pass not yet written idle).
+                const bool flush = (p & 1) || p + 1 == P || ((p + 1) * W + wv) * 64 >= nchunks;
+                if (flush) {
+                    wave_sync();
+                    const int pp = (p & ~1) + (lane >> 5);
+                    const int ch = 2 * (lane & 31);                       // first chunk of the group in pass pp
+                    const int cg = (pp * W + wv) * 64 + ch;               // its chunk in the row
+                    const bool live = pp <= p && cg < nchunks;
+                    uint4 gq[4];
+                    if (live) {
 #pragma unroll
-                    for (int h = 0; h < 4; ++h) gq[h] = reinterpret_cast<const uint4*>(b6_slot(lane, 0))[h];
+                        for (int h = 0; h < 4; ++h) gq[h] = reinterpret_cast<const uint4*>(b6_slot(ch, 0, pp & 1))[h];
+                    }
+                    wave_sync();
+                    if (live) {
+                        const v16u words = {gq[0].x, gq[0].y, gq[0].z, gq[0].w, gq[1].x, gq[1].y, gq[1].z, gq[1].w,
+                                            gq[2].x, gq[2].y, gq[2].z, gq[2].w, gq[3].x, gq[3].y, gq[3].z, gq[3].w};
+                        const v6u r = __builtin_amdgcn_cvt_scalef32_pk32_bf6_bf16(__builtin_bit_cast(v32bf, words), 1.0f);
+                        const uint32_t d[6] = {r[0], r[1], r[2], r[3], r[4], r[5]};
+                        b6_store_group(qout, row, K, cg * kChunk, d);
+                    }
                 }
-            } else {
-                w = reinterpret_cast<const uint4*>(cb)[lane];
+                continue;
             }
+            wave_sync();
+            const uint4 w = reinterpret_cast<const uint4*>(cb)[lane];
             wave_sync();
             if (OUT == OUT_I8 && ok) {
                 *reinterpret_cast<uint4*>(qout + (size_t)row * K + (size_t)c * kChunk) = w;
@@ -665,17 +686,6 @@ __global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
                 const int k0 = c * kChunk;
                 int8_t* chunk = qout + ((size_t)(row >> 8) * (K >> 6) + (k0 >> 6)) * I8T_CHUNK;
                 *reinterpret_cast<uint4*>(chunk + i8t_off(row & 255, (k0 >> 4) & 3)) = w;
-            } else if (B6 && ok) {
-                // chunks (2g', 2g'+1) are the 32 codes of one MFMA group: the even lane
-                // converts them (bf16 values, element order) with the 32-wide BF6
-                // converter and stores the group's 6 dwords
-                if ((lane & 1) == 0) {
-                    const v16u words = {gq[0].x, gq[0].y, gq[0].z, gq[0].w, gq[1].x, gq[1].y, gq[1].z, gq[1].w,
-                                        gq[2].x, gq[2].y, gq[2].z, gq[2].w, gq[3].x, gq[3].y, gq[3].z, gq[3].w};
-                    const v6u r = __builtin_amdgcn_cvt_scalef32_pk32_bf6_bf16(__builtin_bit_cast(v32bf, words), 1.0f);
-                    const uint32_t d[6] = {r[0], r[1], r[2], r[3], r[4], r[5]};
-                    b6_store_group(qout, row, K, c * kChunk, d);
-                }
             } else if (ok) {
                 const uint32_t ws[4] = {w.x & 0x0f0f0f0fu, w.y & 0x0f0f0f0fu, w.z & 0x0f0f0f0fu,
                                         w.w & 0x0f0f0f0fu};
