@@ -306,6 +306,23 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
         const int col = col0 + cc * EPC;
         const int rl0 = lane / CW;
         uint8_t* orow = reinterpret_cast<uint8_t*>(out) + ((size_t)(row0 + i0 * 32 + rl0) * N + col) * ES;
+        // A pass whose 32 rows and whose wave-tile columns all lie inside the
+        // output (16-byte aligned rows): every lane stores every chunk, so its
+        // LDS reads go out together and one wait covers them, instead of one
+        // read, wait and bounds-checked store after another.  Wave-uniform.
+        if (EPI != EPI_ATOMIC_ACC && vec && row0 + i0 * 32 + PT * 32 <= M && col0 + FNT * 32 <= N) {
+            uint4 d[NCH / 64];
+#pragma unroll
+            for (int q = 0; q < NCH / 64; ++q)
+                d[q] = *reinterpret_cast<const uint4*>(scr + (rl0 + q * RSTEP) * RS + cc * 16);
+            typedef unsigned v4u_st __attribute__((ext_vector_type(4)));
+#pragma unroll
+            for (int q = 0; q < NCH / 64; ++q)
+                __builtin_nontemporal_store((v4u_st){d[q].x, d[q].y, d[q].z, d[q].w},
+                                            reinterpret_cast<v4u_st*>(orow + (size_t)q * RSTEP * N * ES));
+            wave_sync();
+            continue;
+        }
 #pragma unroll
         for (int q0 = 0; q0 < NCH; q0 += 64) {
             const int rl = rl0 + (q0 / 64) * RSTEP;
