@@ -176,3 +176,27 @@ def test_linear_replayed_from_hip_graph(backend, native, gpu, M, N, K, R):
             torch.cuda.synchronize()
             assert torch.equal(y, want[i]), (rep, i)
             assert torch.equal(eager, want[(i + 1) % len(xs)]), (rep, i)
+
+
+@pytest.mark.parametrize("lora", [False, True])
+def test_strided_and_batched_inputs_equal_contiguous(backend, native, gpu, lora):
+    """A strided view (every other row of a wider buffer, a transposed copy) and
+    a [batch, tokens, features] activation give the bits of the same values
+    passed contiguous and 2-D, with and without a LoRA."""
+    N, K, B, T = 640, 3072, 3, 300
+    G = backend.pick_groupsize(K)
+    qw, ws = backend.quantize_convrot_w4a4_weight(normal_weight(N, K, seed=31).cuda(), convrot_groupsize=G)
+    b = normal_bias(N, seed=32).cuda()
+    pair = _lora_pair(N, K, 32, 33) if lora else None
+    x3 = outlier_activations(B * T, K, seed=34).reshape(B, T, K).cuda()
+    y3 = backend.convrot_w4a4_linear(x3, qw, ws, bias=b, convrot_groupsize=G, lora=pair)
+    assert y3.shape == (B, T, N)
+    y2 = backend.convrot_w4a4_linear(x3.reshape(B * T, K).contiguous(), qw, ws, bias=b, convrot_groupsize=G, lora=pair)
+    assert torch.equal(y3.reshape(B * T, N), y2)
+    wide = torch.zeros(2 * B * T, K, dtype=x3.dtype, device="cuda")
+    wide[::2] = x3.reshape(B * T, K)
+    ys = backend.convrot_w4a4_linear(wide[::2], qw, ws, bias=b, convrot_groupsize=G, lora=pair)
+    assert torch.equal(ys, y2)
+    xt = x3.reshape(B * T, K).t().contiguous().t()                # column-major storage of the same values
+    yt = backend.convrot_w4a4_linear(xt, qw, ws, bias=b, convrot_groupsize=G, lora=pair)
+    assert torch.equal(yt, y2)
