@@ -40,6 +40,7 @@ __all__ = [
     "bf6_path_ok",
     "i8t_path_ok",
     "prepare_convrot_w8a8_weight_i8t",
+    "max_quant_k",
 ]
 
 # largest concatenated rank of the fused LoRA side path (padded to a multiple of 32)
@@ -82,6 +83,20 @@ def validate_w4a4_shape(tensor: torch.Tensor, convrot_groupsize: int, quant_grou
         raise ValueError(f"in_features {k} not divisible by quant_group_size {quant_group_size}")
 
 
+def max_quant_k() -> int:
+    """Widest row (in_features) the fused rotate+quantize kernels take: 32768."""
+    return native.max_quant_k()
+
+
+def _check_width(k: int) -> None:
+    """Rows wider than the fused kernels take raise here, with the reason, so a
+    loader that catches the error keeps the layer in bf16 (the reference's
+    dispatcher instead rotates such rows with torch, _int4/__init__.py:59-66)."""
+    cap = max_quant_k()
+    if k > cap:
+        raise ValueError(f"in_features {k} exceeds {cap}, the widest row the gfx950 rotate+quantize kernels take")
+
+
 def _on_gpu(t: torch.Tensor) -> torch.Tensor:
     if t.is_cuda:
         return t
@@ -109,6 +124,7 @@ def quantize_convrot_w4a4_weight(
         raise ValueError(f"int4 MMA kernel requires quant_group_size {_INT4_GROUP_SIZE}")
     validate_w4a4_shape(weight, convrot_groupsize, quant_group_size)
     _check_groupsize(convrot_groupsize)
+    _check_width(weight.shape[-1])
     dev = weight.device
     w = _on_gpu(weight).contiguous()
     if w.dtype not in (torch.float16, torch.bfloat16, torch.float32):
@@ -237,6 +253,7 @@ def convrot_w4a4_linear(
     if x.shape[-1] % convrot_groupsize != 0:
         raise ValueError(f"Input K={x.shape[-1]} not divisible by convrot_groupsize {convrot_groupsize}")
     _check_groupsize(convrot_groupsize)
+    _check_width(x.shape[-1])
 
     orig_shape = x.shape
     x2d = x.reshape(-1, orig_shape[-1]).contiguous()
@@ -369,6 +386,7 @@ def convrot_w8a8_linear(
     if x.shape[-1] % convrot_groupsize != 0:
         raise ValueError(f"Input K={x.shape[-1]} not divisible by convrot_groupsize {convrot_groupsize}")
     _check_groupsize(convrot_groupsize)
+    _check_width(x.shape[-1])
     orig_shape = x.shape
     x2d = x.reshape(-1, orig_shape[-1]).contiguous()
     if x2d.dtype not in native._IN_DTYPE_CODE:

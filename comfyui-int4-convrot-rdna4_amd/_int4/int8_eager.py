@@ -13,7 +13,7 @@ from __future__ import annotations
 
 import torch
 
-from . import _check_groupsize, _hadamard, _on_gpu, convrot_w8a8_linear, native
+from . import _check_groupsize, _check_width, _hadamard, _on_gpu, convrot_w8a8_linear, native
 
 __all__ = ["quantize_convrot_w8a8_weight", "dequantize_convrot_w8a8_weight", "convrot_w8a8_linear"]
 
@@ -32,6 +32,7 @@ def quantize_convrot_w8a8_weight(
         raise ValueError(f"in_features {weight.shape[-1]} not divisible by "
                          f"convrot_groupsize {convrot_groupsize}")
     _check_groupsize(convrot_groupsize)
+    _check_width(weight.shape[-1])
     dev = weight.device
     w = _on_gpu(weight).contiguous()
     if w.dtype not in (torch.float16, torch.bfloat16, torch.float32):

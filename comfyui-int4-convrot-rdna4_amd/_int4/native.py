@@ -30,7 +30,7 @@ _IN_DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 EPI_F32, EPI_BF16, EPI_BF16_EAGER, EPI_ACC = 0, 1, 2, 3
 
 # cr_abi_version() of the library these signatures describe
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _vp, _i = ctypes.c_void_p, ctypes.c_int
 _SIGNATURES = {
@@ -43,6 +43,7 @@ _SIGNATURES = {
     "cr_lora_down_workspace": ([_i, _i, _i], ctypes.c_size_t),
     "cr_int4_convrot_gemm_lora": ([_vp] * 7 + [_i, ctypes.c_float, _vp] + [_i] * 4 + [_vp], _i),
     "cr_int4_to_bf6": ([_vp, _vp, _i, _i, _vp], _i),
+    "cr_bf6_to_int4": ([_vp, _vp, _i, _i, _vp], _i),
     "cr_convrot_quant_bf6": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
     "cr_max_quant_bf6_k": ([], _i),
     "cr_int4_convrot_gemm_bf6": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
@@ -52,6 +53,7 @@ _SIGNATURES = {
     "cr_int8_convrot_gemm_ex": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
     "cr_convrot_quant_int8_i8t": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp], _i),
     "cr_int8_to_i8t": ([_vp, _vp, _i, _i, _vp], _i),
+    "cr_i8t_to_int8": ([_vp, _vp, _i, _i, _vp], _i),
     "cr_int8_convrot_gemm_i8t": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
     "cr_gemm_bf6_choose_nsplit": ([_i, _i, _i], _i),
     "cr_gemm_bf6_splitk_workspace": ([_i, _i, _i], ctypes.c_size_t),
@@ -386,6 +388,22 @@ def int4_to_bf6(packed: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def bf6_to_int4(a6: torch.Tensor, rows: int, K: int) -> torch.Tensor:
+    """B6T operand -> packed int4 [rows, K/2] (the inverse of int4_to_bf6 on the
+    first ``rows`` rows, bit for bit)."""
+    lib = load_library()
+    _check_cuda(a6)
+    if a6.dtype != torch.uint8 or a6.shape != (bf6_rows(rows), K // 4 * 3) or K % 128 != 0:
+        raise ValueError(f"a B6T operand of a [{rows}, {K}] matrix is uint8 [{bf6_rows(rows)}, {K // 4 * 3}], "
+                         f"got {a6.dtype} {tuple(a6.shape)}")
+    a6 = _aligned(a6)
+    out = torch.empty((rows, K // 2), dtype=torch.int8, device=a6.device)
+    rc = lib.cr_bf6_to_int4(_ptr(a6), _ptr(out), rows, K, _stream(a6.device))
+    if rc != 0:
+        raise RuntimeError(f"cr_bf6_to_int4 failed, hipError={rc}")
+    return out
+
+
 def max_quant_bf6_k() -> int:
     return _limit("cr_max_quant_bf6_k")
 
@@ -580,6 +598,23 @@ def int8_to_i8t(q: torch.Tensor) -> torch.Tensor:
     rc = lib.cr_int8_to_i8t(_ptr(q), _ptr(out), rows, K, _stream(q.device))
     if rc != 0:
         raise RuntimeError(f"cr_int8_to_i8t failed, hipError={rc}")
+    return out
+
+
+def i8t_to_int8(q8t: torch.Tensor, rows: int) -> torch.Tensor:
+    """I8T operand -> row-major int8 [rows, K] (the inverse of int8_to_i8t on
+    the first ``rows`` rows)."""
+    lib = load_library()
+    _check_cuda(q8t)
+    K = q8t.shape[-1]
+    if q8t.dtype != torch.int8 or q8t.shape != (i8t_rows(rows), K) or K % 64 != 0:
+        raise ValueError(f"an I8T operand of {rows} rows is int8 [{i8t_rows(rows)}, K], got {q8t.dtype} "
+                         f"{tuple(q8t.shape)}")
+    q8t = _aligned(q8t)
+    out = torch.empty((rows, K), dtype=torch.int8, device=q8t.device)
+    rc = lib.cr_i8t_to_int8(_ptr(q8t), _ptr(out), rows, K, _stream(q8t.device))
+    if rc != 0:
+        raise RuntimeError(f"cr_i8t_to_int8 failed, hipError={rc}")
     return out
 
 

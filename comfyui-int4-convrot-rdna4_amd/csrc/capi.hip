@@ -18,6 +18,8 @@ hipError_t lora_down_launch(const void* x, int in_dtype, const void* D, void* t,
 hipError_t lora_part_launch(const void* x, int in_dtype, const void* D, float* part, void* t, int M, int K, int R,
                             int* splits, hipStream_t st);
 hipError_t int4_to_bf6_launch(const void* src, void* dst, int rows, int K, hipStream_t st);
+hipError_t bf6_to_int4_launch(const void* src, void* dst, int rows, int K, hipStream_t st);
+hipError_t i8t_to_int8_launch(const void* src, void* dst, int rows, int K, hipStream_t st);
 hipError_t rotquant_b6_launch(const void* x, int in_dtype, uint8_t* a6, float* s, int M, int K, int G,
                               hipStream_t st, const LoraSum* ls);
 int rotquant_b6_max_k();
@@ -133,6 +135,11 @@ API int cr_int4_to_bf6(const void* src, void* dst, int rows, int K, void* stream
     return (int)convrot::int4_to_bf6_launch(src, dst, rows, K, reinterpret_cast<hipStream_t>(stream));
 }
 
+API int cr_bf6_to_int4(const void* src, void* dst, int rows, int K, void* stream) {
+    if (rows < 0 || !bf6_k_ok(K)) return -1;
+    return (int)convrot::bf6_to_int4_launch(src, dst, rows, K, reinterpret_cast<hipStream_t>(stream));
+}
+
 API int cr_convrot_quant_bf6(const void* x, int in_dtype, void* a6out, void* scaleout, int M, int K, int G,
                              void* stream) {
     if (!quant_args_ok(in_dtype, M, K, G) || K % 128 != 0 || K > convrot::rotquant_b6_max_k()) return -1;
@@ -226,6 +233,11 @@ API int cr_convrot_quant_int8_i8t(const void* x, int in_dtype, void* qout, void*
 API int cr_int8_to_i8t(const void* src, void* dst, int rows, int K, void* stream) {
     if (rows < 0 || !i8t_k_ok(K)) return -1;
     return (int)convrot::int8_to_i8t_launch(src, dst, rows, K, reinterpret_cast<hipStream_t>(stream));
+}
+
+API int cr_i8t_to_int8(const void* src, void* dst, int rows, int K, void* stream) {
+    if (rows < 0 || !i8t_k_ok(K)) return -1;
+    return (int)convrot::i8t_to_int8_launch(src, dst, rows, K, reinterpret_cast<hipStream_t>(stream));
 }
 
 API int cr_int8_convrot_gemm_i8t(const void* X, const void* W, const void* xscale, const void* wscale,
@@ -359,4 +371,4 @@ API int cr_convrot_w4a4_linear_bf6_noalloc(const void* x, int in_dtype, const vo
 
 API int cr_max_quant_k(void) { return convrot::rotquant_max_k(); }
 
-API int cr_abi_version(void) { return 9; }
+API int cr_abi_version(void) { return 10; }

@@ -529,6 +529,29 @@ hipError_t int8_to_i8t_launch(const void* src, void* dst, int rows, int K, hipSt
     return hipGetLastError();
 }
 
+// I8T -> row-major int8 [rows, K] (the inverse of int8_to_i8t_kernel on the
+// first `rows` rows): one thread per (row, 16-byte piece).
+__global__ __launch_bounds__(256) void i8t_to_int8_kernel(const int8_t* __restrict__ src, int8_t* __restrict__ dst,
+                                                          int rows, int K) {
+    const int np = K / 16;
+    const long long id = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (id >= (long long)rows * np) return;
+    const int row = (int)(id / np), pc = (int)(id % np);
+    const int kb = pc >> 2, c = pc & 3;
+    const int8_t* chunk = src + ((size_t)(row >> 8) * (K / 64) + kb) * I8T_CHUNK;
+    *reinterpret_cast<uint4*>(dst + (size_t)row * K + (size_t)pc * 16) =
+        *reinterpret_cast<const uint4*>(chunk + i8t_off(row & 255, c));
+}
+
+hipError_t i8t_to_int8_launch(const void* src, void* dst, int rows, int K, hipStream_t st) {
+    if (rows < 0 || K <= 0 || K % 64 != 0) return hipErrorInvalidValue;
+    if (rows == 0) return hipSuccess;
+    const long long n = (long long)rows * (K / 16);
+    hipLaunchKernelGGL(i8t_to_int8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       reinterpret_cast<const int8_t*>(src), reinterpret_cast<int8_t*>(dst), rows, K);
+    return hipGetLastError();
+}
+
 // Split-K finalize: accum holds the exact int32 accumulators (the sum of every
 // split's partial); each becomes fl32(fl32(float(acc) * xs[m]) * ws[n]) in
 // place, the unsplit f32 epilogue without its bias term.

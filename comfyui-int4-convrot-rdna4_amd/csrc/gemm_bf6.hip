@@ -88,6 +88,43 @@ __global__ __launch_bounds__(256) void int4_to_bf6t_kernel(const uint8_t* __rest
     }
 }
 
+// integer value of a BF6 code that holds an int4 value (0 and -0 -> 0,
+// |v| = (4 + m) 2^(e - 5) for exponent field e >= 3, sign bit 0x20)
+__device__ __forceinline__ int int_of_bf6(uint32_t c) {
+    const int e = (int)((c >> 2) & 7), m = (int)(c & 3);
+    const int a = e < 3 ? 0 : ((4 + m) << e) >> 5;
+    return (c & 0x20u) ? -a : a;
+}
+
+// B6T -> packed int4 [rows, K/2] (the inverse of int4_to_bf6t_kernel on the
+// first `rows` rows): one thread per (row, 32-code group), 16 bytes out.
+__global__ __launch_bounds__(256) void bf6t_to_int4_kernel(const uint8_t* __restrict__ src,
+                                                           uint8_t* __restrict__ dst, int rows, int K) {
+    const int ng = K / 32;
+    const long long id = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (id >= (long long)rows * ng) return;
+    const int row = (int)(id / ng), gi = (int)(id % ng);
+    const int kb = gi >> 2, g = gi & 3, r = row & 255;
+    const uint8_t* chunk = src + ((size_t)(row >> 8) * (K / 128) + kb) * B6_CHUNK;
+    const uint4 p = *reinterpret_cast<const uint4*>(chunk + b6_p_off(r, g));
+    const uint4 q = *reinterpret_cast<const uint4*>(chunk + b6_q_off(r, g));
+    uint32_t d[6];
+    if (!b6_odd_tile(r)) {          // P = d0..d3, Q bytes 0..7 = d4..d5
+        d[0] = p.x; d[1] = p.y; d[2] = p.z; d[3] = p.w; d[4] = q.x; d[5] = q.y;
+    } else {                        // P = d2..d5, Q bytes 8..15 = d0..d1
+        d[0] = q.z; d[1] = q.w; d[2] = p.x; d[3] = p.y; d[4] = p.z; d[5] = p.w;
+    }
+    uint32_t o[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+        const int bit = 6 * e;
+        uint32_t c = d[bit >> 5] >> (bit & 31);
+        if ((bit & 31) > 26) c |= d[(bit >> 5) + 1] << (32 - (bit & 31));
+        o[e >> 3] |= ((uint32_t)int_of_bf6(c & 63u) & 15u) << ((e & 7) * 4);
+    }
+    *reinterpret_cast<uint4*>(dst + (size_t)row * (K / 2) + (size_t)gi * 16) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 // ---------------------------------------------------------------------------
 // GEMM: 256 x 256 tile per workgroup of 8 waves (2 along M x 4 along N, wave
 // tile 128 x 64 = 4 x 2 MFMA tiles of 32 x 32).  A stage is the A chunk and
@@ -615,6 +652,14 @@ hipError_t int4_to_bf6_launch(const void* src, void* dst, int rows, int K, hipSt
     if (rows == 0) return hipSuccess;
     const long long n = (long long)((rows + 255) / 256) * (K / 128) * 256;
     hipLaunchKernelGGL(int4_to_bf6t_kernel, dim3((unsigned)(n / 256)), dim3(256), 0, st,
+                       reinterpret_cast<const uint8_t*>(src), reinterpret_cast<uint8_t*>(dst), rows, K);
+    return hipGetLastError();
+}
+
+hipError_t bf6_to_int4_launch(const void* src, void* dst, int rows, int K, hipStream_t st) {
+    if (rows == 0) return hipSuccess;
+    const long long n = (long long)rows * (K / 32);
+    hipLaunchKernelGGL(bf6t_to_int4_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                        reinterpret_cast<const uint8_t*>(src), reinterpret_cast<uint8_t*>(dst), rows, K);
     return hipGetLastError();
 }

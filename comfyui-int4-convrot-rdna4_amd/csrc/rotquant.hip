@@ -276,7 +276,7 @@ __global__ __launch_bounds__(kMaxThreads) void rotquant_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Row-split kernel (K <= 12288).
+// Row-split kernel (K <= 32768).
 //
 // A workgroup of W waves quantizes one row at a time and walks rows
 // persistently (blockIdx.x, + gridDim.x, ...).  A row of K elements is K/16
@@ -292,7 +292,8 @@ __global__ __launch_bounds__(kMaxThreads) void rotquant_kernel(
 // waves running a whole row each while the rest of the chip idles.
 // ---------------------------------------------------------------------------
 
-constexpr int kRowMaxWaves = 4;                        // waves per workgroup
+constexpr int kRowMaxWaves = 4;                        // waves per workgroup, rows of up to 12288
+constexpr int kRowWideWaves = 16;                      // waves per workgroup, rows of up to 32768
 constexpr int kRowMaxPass = 6;                         // passes per wave
 constexpr int kRowWaveLds = 64 * kPad * 8;             // LDS bytes per wave
 
@@ -491,8 +492,10 @@ __device__ __forceinline__ float fmax3(float a, float b, float c) {
 // LR: also finish the linear's LoRA down projection for every row (LoraSum):
 // wave 0 loads the row's partials at the start of the row and stores their sum
 // after the row's codes, so the loads' latency hides behind the rotation.
-template <int DT, int G, int P, int OUT, bool LR>
-__global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
+// MAXW: the largest workgroup (in waves) the instance serves; RS = 8 or 16
+// row-absmax slots per row parity.
+template <int DT, int G, int P, int OUT, bool LR, int MAXW = kRowMaxWaves>
+__global__ __launch_bounds__(64 * MAXW) void rotquant_row_kernel(
         const void* __restrict__ x, int8_t* __restrict__ qout, float* __restrict__ sout, int M, int K,
         LoraSum ls) {
     constexpr int LPG = G / kChunk;
@@ -506,7 +509,9 @@ __global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
     // chunk ch at (ch / 16) * 544 + (ch % 16) * 32 bytes (the pad spreads the
     // four 16-lane groups over the banks), one region per pass parity so that
     // two passes are converted together.  After the W wave buffers: the
-    // per-wave row absmax, 8 slots per row parity (slots W..7 hold zeros).
+    // per-wave row absmax, RS slots per row parity (slots W..RS-1 hold zeros).
+    constexpr int RS = MAXW <= 8 ? 8 : 16;
+    static_assert(MAXW <= 16, "row absmax slots");
     constexpr int kB6Group = 544;
     constexpr int kB6Region = 4 * kB6Group;
     static_assert(kRowWaveLds >= (B6 ? 2 * kB6Region : 64 * 16), "code buffer");
@@ -525,7 +530,7 @@ __global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
     const int gl = lane % LPG;
     const int gfirst = lane - gl;
     const float kMagic = 12582912.0f;
-    if (wv == 0 && lane < 16 && (lane & 7) >= W) red[lane] = 0.0f;   // before the first barrier
+    if (wv == 0 && lane < 2 * RS && (lane & (RS - 1)) >= W) red[lane] = 0.0f;   // before the first barrier
 
     // One chunk buffer, loaded one pass ahead: while pass p is rotated, the
     // wave already loads its next live pass of the row, or its first pass of
@@ -579,12 +584,18 @@ __global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
         // v_max3 drops NaN operands), then across the W waves
         lmax = wave_max_nonneg(lmax);
         if (W > 1) {
-            float* rb = red + (it & 1) * 8;
+            float* rb = red + (it & 1) * RS;
             if (lane == 0) rb[wv] = lmax;
             __syncthreads();
             const float4 r0 = reinterpret_cast<const float4*>(rb)[0];
             const float4 r1 = reinterpret_cast<const float4*>(rb)[1];
             lmax = fmax3(fmax3(r0.x, r0.y, r0.z), fmax3(r0.w, r1.x, r1.y), fmax3(r1.z, r1.w, 0.0f));
+            if constexpr (RS == 16) {
+                const float4 r2 = reinterpret_cast<const float4*>(rb)[2];
+                const float4 r3 = reinterpret_cast<const float4*>(rb)[3];
+                lmax = fmax3(lmax, fmax3(r2.x, r2.y, r2.z), fmax3(r2.w, r3.x, r3.y));
+                lmax = fmax3(lmax, r3.z, r3.w);
+            }
         }
         const float a = fmaxf(round_to_dt<DT>(lmax), clamp_floor<DT>());
         // s = RNE_DT(fl32(a / QMAX)).  a is a DT value of p <= 11 significant
@@ -747,11 +758,37 @@ __global__ __launch_bounds__(64 * kRowMaxWaves) void rotquant_row_kernel(
 // M = 2048 22.5 / 26.3 us, 4096 39.3 / 42.4, 4608 43.4 / 45.4, 16384 142.1 /
 // 144.1 (K = 9216: 3 x 3 against 2 x 5, 3-8% faster).  One workgroup per row
 // (below).
+// Rows of 13 to 32 passes (K in (12288, 32768]): 8 waves of 2 or 3 passes, or
+// 16 waves of 2, on the 16-wave instance (8.7 KB of LDS per wave, so one
+// 16-wave or two 8-wave workgroups fill a CU's 16 wave slots).
+template <int DT, int G, int P, int OUT, bool LR>
+static hipError_t rq_wide_launch(const void* x, int8_t* q, float* s, int M, int K, int W, hipStream_t st,
+                                 const LoraSum& ls) {
+    static std::atomic<bool> attr_set[kMaxDev];
+    void (*kern)(const void*, int8_t*, float*, int, int, LoraSum) =
+        rotquant_row_kernel<DT, G, P, OUT, LR, kRowWideWaves>;
+    int dev = 0;
+    hipError_t e = current_device(&dev);
+    if (e != hipSuccess) return e;
+    e = lds_limit_once(attr_set, dev, reinterpret_cast<const void*>(kern),
+                       kRowWideWaves * kRowWaveLds + 32 * (int)sizeof(float));
+    if (e != hipSuccess) return e;
+    const size_t lds = (size_t)W * kRowWaveLds + 32 * sizeof(float);
+    hipLaunchKernelGGL(kern, dim3(M), dim3(64 * W), lds, st, x, q, s, M, K, ls);
+    return hipGetLastError();
+}
+
 template <int DT, int G, int OUT, bool LR = false>
 static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K, hipStream_t st,
                                 const LoraSum& ls = LoraSum{}) {
     if (M <= 0) return hipSuccess;
     const int np = (K / kChunk + 63) / 64;
+    if (np > 3 * kRowMaxWaves) {
+        if (np > 2 * kRowWideWaves) return hipErrorInvalidValue;
+        if (np <= 16) return rq_wide_launch<DT, G, 2, OUT, LR>(x, q, s, M, K, 8, st, ls);
+        if (np <= 24) return rq_wide_launch<DT, G, 3, OUT, LR>(x, q, s, M, K, 8, st, ls);
+        return rq_wide_launch<DT, G, 2, OUT, LR>(x, q, s, M, K, 16, st, ls);
+    }
     int W, P;
     if (np <= 2 * kRowMaxWaves) {
         P = np <= kRowMaxWaves ? np : (np % 3 != 0 ? 2 : 3);
@@ -790,7 +827,7 @@ static hipError_t rq_row_launch(const void* x, int8_t* q, float* s, int M, int K
     return hipGetLastError();
 }
 
-constexpr int kWaveMaxK = 12 * 64 * kChunk;   // 12288: 4 waves x 3 passes
+constexpr int kRowMaxK = 2 * kRowWideWaves * 64 * kChunk;   // 32768: 16 waves x 2 passes
 
 // ---------------------------------------------------------------------------
 // host-side launch
@@ -819,7 +856,7 @@ template <int DT, int G, bool STOCH, bool I8 = false>
 static hipError_t rq_launch_g(const void* x, const void* noise, int8_t* q, float* s, int M, int K,
                               hipStream_t st) {
     if (M == 0) return hipSuccess;
-    if (!STOCH && K <= kWaveMaxK) return rq_row_launch<DT, G, I8 ? OUT_I8 : OUT_PACK4>(x, q, s, M, K, st);
+    if (!STOCH && K <= kRowMaxK) return rq_row_launch<DT, G, I8 ? OUT_I8 : OUT_PACK4>(x, q, s, M, K, st);
     RQPlan pl;
     if (rq_plan(M, K, G, &pl) != 0) return hipErrorInvalidValue;
     dim3 grid(pl.grid), block(pl.block);
@@ -863,11 +900,11 @@ hipError_t rotquant_launch(const void* x, int in_dtype, const void* noise, int8_
 
 int rotquant_max_k() { return 8 * kMaxThreads * kChunk; }
 
-// fused rotate + quantize into the B6T layout (K % 128 == 0, K <= 12288)
+// fused rotate + quantize into the B6T layout (K % 128 == 0, K <= 32768)
 // With `ls` (not null) the kernel also sums the LoRA partials of every row into ls->t.
 hipError_t rotquant_b6_launch(const void* x, int in_dtype, uint8_t* a6, float* s, int M, int K, int G,
                               hipStream_t st, const LoraSum* ls) {
-    if (K % 128 != 0 || K > kWaveMaxK || M < 0) return hipErrorInvalidValue;
+    if (K % 128 != 0 || K > kRowMaxK || M < 0) return hipErrorInvalidValue;
     if (ls != nullptr && (ls->S < 1 || ls->S > 8 || ls->R < 1 || ls->part == nullptr || ls->t == nullptr))
         return hipErrorInvalidValue;
     int8_t* q = reinterpret_cast<int8_t*>(a6);
@@ -890,12 +927,12 @@ hipError_t rotquant_b6_launch(const void* x, int in_dtype, uint8_t* a6, float* s
 #undef RB6_G
 }
 
-int rotquant_b6_max_k() { return kWaveMaxK; }
+int rotquant_b6_max_k() { return kRowMaxK; }
 
-// fused rotate + int8 quantize into the I8T layout (K % 64 == 0, K <= 12288)
+// fused rotate + int8 quantize into the I8T layout (K % 64 == 0, K <= 32768)
 hipError_t rotquant_i8t_launch(const void* x, int in_dtype, int8_t* q, float* s, int M, int K, int G,
                                hipStream_t st) {
-    if (K % 64 != 0 || K > kWaveMaxK || M < 0) return hipErrorInvalidValue;
+    if (K % 64 != 0 || K > kRowMaxK || M < 0) return hipErrorInvalidValue;
 #define RI8T_G(DT)                                                                                  \
     switch (G) {                                                                                    \
         case 16: return rq_row_launch<DT, 16, OUT_I8T>(x, q, s, M, K, st);                         \

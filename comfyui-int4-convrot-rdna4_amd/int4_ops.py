@@ -190,14 +190,36 @@ if _COMFY_OPS and _CK_OK:
                     _meta_skeleton(self, in_features, out_features, bias, dtype)
                 else:
                     super().__init__(in_features, out_features, bias, device, dtype)
-                # quantized storage (None: a plain layer)
+                # quantized storage (None: a plain layer); see the _q property
                 self._q = self._qs = self._qgs = self._qmode = None
                 self._q6 = None       # int4 weight as the bf6 GEMM's operand (made at load time)
                 self._q8t = None      # int8 weight as the tile-major W8A8 GEMM's operand
+                self._qshape = None   # shape stand-in of _q (meta device) for the linear's checks
                 # dynamic LoRA: every attached adapter, the plain ones fused into one
                 # (D, U) pair for the GEMM epilogue, and the rest (h() side path)
                 self._dyn_lora = self._dyn_fused = self._dyn_rest = None
                 self.comfy_cast_weights = False
+
+            # One copy of a quantized weight stays on the device: the GEMM's
+            # operand.  When that is the B6T (int4) or I8T (int8) tile layout,
+            # `_q`, the checkpoint layout (packed int4 [N, K/2] or int8 [N, K])
+            # that the Save node reads (int4_save.py:113-119), is decoded from it
+            # on each read, bit for bit, on the operand's device; otherwise the
+            # checkpoint layout is the operand itself (`_qpack`).
+            @property
+            def _q(self):
+                if self._qpack is not None:
+                    return self._qpack
+                if self._q6 is not None:
+                    return _ck.native.bf6_to_int4(self._q6, self.out_features, self.in_features)
+                if self._q8t is not None:
+                    return _ck.native.i8t_to_int8(self._q8t, self.out_features)
+                return None
+
+            @_q.setter
+            def _q(self, value):
+                self._qpack = value
+                self._q6 = self._q8t = None
 
             _normalize_lora_key = staticmethod(_strip_prefix)
 
@@ -284,7 +306,8 @@ if _COMFY_OPS and _CK_OK:
                 ops = Int4ConvRotOps
                 eligible = (ops.enable and w is not None and w.dim() == 2
                             and self.in_features >= ops.min_in_features
-                            and _pick_groupsize(self.in_features) is not None)
+                            and _pick_groupsize(self.in_features) is not None
+                            and self.in_features <= _ck.max_quant_k())
                 if not eligible or any(n in prefix for n in ops.excluded_names or ()):
                     return False
                 return self._exact_key(prefix) not in ops.excluded_exact
@@ -295,15 +318,19 @@ if _COMFY_OPS and _CK_OK:
             # -- load-time state ------------------------------------------------
 
             def _install(self, q, scale, groupsize, mode, state_dict, keys, consumed):
-                """Take over quantized storage (on the GPU): the checkpoint copy,
-                the GEMM operand made from it, and the bias in fp16; the
-                `consumed` keys leave state_dict."""
+                """Take over quantized storage (on the GPU): the GEMM operand
+                made from the checkpoint-layout codes `q` (which are dropped
+                when the operand is a tile layout), the scales, and the bias in
+                fp16; the `consumed` keys leave state_dict."""
                 dev = torch.device("cuda")
-                self._q = q.to(dev).contiguous()
+                q = q.to(dev).contiguous()
                 self._qs = scale.to(dev, torch.float32).reshape(-1).contiguous()
                 self._qgs, self._qmode = groupsize, mode
-                self._q6 = _ck.prepare_convrot_w4a4_weight_bf6(self._q) if mode == "int4" else None
-                self._q8t = _ck.prepare_convrot_w8a8_weight_i8t(self._q) if mode == "int8" else None
+                q6 = _ck.prepare_convrot_w4a4_weight_bf6(q) if mode == "int4" else None
+                q8t = _ck.prepare_convrot_w8a8_weight_i8t(q) if mode == "int8" else None
+                self._q = q if q6 is None and q8t is None else None
+                self._q6, self._q8t = q6, q8t
+                self._qshape = torch.empty(tuple(q.shape), dtype=torch.int8, device="meta")
                 self.weight = None
                 for k in consumed:
                     state_dict.pop(k, None)
@@ -329,6 +356,18 @@ if _COMFY_OPS and _CK_OK:
                         return False
                 groupsize = groupsize or _pick_groupsize(self.in_features)
                 if groupsize is None:
+                    return False
+                if self.in_features > _ck.max_quant_k():
+                    # rows too wide for the fused quantizer: keep the layer in bf16,
+                    # from the stored codes (the reference rotates such rows with torch)
+                    logging.warning(f"INT4 ConvRot: {prefix} has in_features {self.in_features} above "
+                                    f"{_ck.max_quant_k()}; loading it dequantized in bf16")
+                    from ._int4.int8_eager import dequantize_convrot_w8a8_weight
+                    deq = (_ck.dequantize_convrot_w4a4_weight(w, state_dict[skey], groupsize) if mode == "int4" else
+                           dequantize_convrot_w8a8_weight(w, state_dict[skey], groupsize))
+                    state_dict[wkey] = deq.to(torch.bfloat16)
+                    for k in (keys.scale, keys.tag):
+                        state_dict.pop(k, None)
                     return False
                 self._install(w, state_dict[skey], groupsize, mode, state_dict, keys,
                               (keys.weight, keys.scale, keys.tag))
@@ -365,6 +404,10 @@ if _COMFY_OPS and _CK_OK:
 
             def _quantize_on_load(self, state_dict, keys, w):
                 if not self._should_quantize(keys.prefix, w):
+                    if Int4ConvRotOps.enable and w is not None and self.in_features > _ck.max_quant_k():
+                        logging.warning(f"INT4 ConvRot: {keys.prefix} stays bf16: in_features {self.in_features} "
+                                        f"exceeds {_ck.max_quant_k()}, the widest row the gfx950 rotate+quantize "
+                                        f"kernels take")
                     return False
                 mode = self._quant_mode(keys.prefix)
                 groupsize = _pick_groupsize(self.in_features)
@@ -389,6 +432,7 @@ if _COMFY_OPS and _CK_OK:
                 w = state_dict.get(keys.weight)
                 if self._take_prequantized(state_dict, keys, w):
                     return
+                w = state_dict.get(keys.weight)          # a too-wide prequantized weight comes back dequantized
                 w = self._route_lora(state_dict, keys, w)
                 if self._quantize_on_load(state_dict, keys, w):
                     return
@@ -397,27 +441,34 @@ if _COMFY_OPS and _CK_OK:
 
             # -- forward ---------------------------------------------------------
 
+            def _operand(self):
+                """The quantized weight the GEMM reads (the one device copy)."""
+                return self._q6 if self._q6 is not None else self._q8t if self._q8t is not None else self._qpack
+
             def _to_device(self, dev):
                 """Move the quantized storage to `dev` once (the loader may keep
                 layers elsewhere until the model runs)."""
-                if self._q.device == dev:
+                if self._operand().device == dev:
                     return
-                self._q, self._qs = self._q.to(dev), self._qs.to(dev)
+                self._qs = self._qs.to(dev)
+                self._qpack = None if self._qpack is None else self._qpack.to(dev)
                 self._q6 = None if self._q6 is None else self._q6.to(dev)
                 self._q8t = None if self._q8t is None else self._q8t.to(dev)
                 if self._dyn_fused is not None:
                     self._dyn_fused = tuple(t.to(dev) for t in self._dyn_fused)
 
             def forward(self, x):
-                if self._q is None:
+                if self._qmode is None:
                     return self._apply_dyn_lora(x, super().forward(x))
                 self._to_device(x.device)
                 bias = self.bias if self.bias is None or self.bias.device == x.device else self.bias.to(x.device)
+                # the checkpoint-layout codes when they are the operand, else their shape
+                qw = self._qpack if self._qpack is not None else self._qshape
                 if self._qmode == "int8":
-                    y = _ck.convrot_w8a8_linear(x, self._q, self._qs, bias=bias, convrot_groupsize=self._qgs,
+                    y = _ck.convrot_w8a8_linear(x, qw, self._qs, bias=bias, convrot_groupsize=self._qgs,
                                                 qweight_i8t=self._q8t)
                     return self._apply_dyn_lora(x, y)
-                y = _ck.convrot_w4a4_linear(x, self._q, self._qs, bias=bias, convrot_groupsize=self._qgs,
+                y = _ck.convrot_w4a4_linear(x, qw, self._qs, bias=bias, convrot_groupsize=self._qgs,
                                             lora=self._dyn_fused, qweight_bf6=self._q6)
                 return self._apply_dyn_lora(x, y, None if self._dyn_fused is None else self._dyn_rest)
 

@@ -9,7 +9,10 @@
  * ck_convrot_quant_int8) exist here with the same names, argument lists and
  * contracts, so that loader binds this library unchanged:
  *   - all pointers are device pointers; the caller allocates every buffer
- *     (outputs included); the library holds no device memory;
+ *     (outputs included) and every entry point works in caller memory only,
+ *     except cr_convrot_w4a4_linear_bf6_noalloc, whose intermediates live in
+ *     a 64 MiB static device array that the library's code object holds on
+ *     every GPU it is loaded on (whether or not that entry point is called);
  *   - work is enqueued asynchronously on `stream` (a hipStream_t, e.g.
  *     torch.cuda.current_stream().cuda_stream); nothing synchronises;
  *   - dtype codes: input 0 = f32, 1 = bf16, 2 = f16; output 0 = f32, 1 = bf16
@@ -159,6 +162,12 @@ int cr_int4_convrot_gemm_lora(const void* Xp, const void* Wp, const void* xscale
  * ceil(rows / 256) * 256 * 3K/4 bytes). */
 int cr_int4_to_bf6(const void* src, void* dst, int rows, int K, void* stream);
 
+/* B6T -> packed int4 [rows, K/2]: the inverse of cr_int4_to_bf6 on the first
+ * `rows` rows, bit for bit.  Lets a layer keep only its B6T weight on the
+ * device and hand out the checkpoint layout (the reference's Save node reads
+ * it, int4_save.py:114-118) when asked.  No counterpart in the reference. */
+int cr_bf6_to_int4(const void* src, void* dst, int rows, int K, void* stream);
+
 /* ck_convrot_quant_int4 writing the codes in the B6T layout (a6out holds
  * ceil(M / 256) * 256 * 3K/4 bytes, padding rows zero) instead of packed
  * nibbles; same codes and scales.  K % 128 == 0 and K <= cr_max_quant_bf6_k(). */
@@ -240,7 +249,10 @@ size_t cr_convrot_w4a4_linear_bf6_workspace(int M, int N, int K, int R);
  * 4608 fits for K <= 12288; M = 16384, K = 12288 does not), and for the same
  * argument errors as cr_convrot_w4a4_linear_bf6.  The array is shared by all
  * calls on one GPU and holds the last call's contents: calls that overlap on
- * one GPU (different streams, or host threads) race.
+ * one GPU (different streams, or host threads) race.  The first call on a
+ * device looks the array's address up and sets the kernels' LDS limits (not
+ * stream operations): make one call per device before capturing the entry
+ * point into a HIP graph; captured calls then replay like eager ones.
  * No counterpart in the reference: for callers that cannot allocate device
  * memory during a forward (code under HIP graph capture, tight serving loops,
  * harnesses that forbid allocation).
@@ -290,12 +302,14 @@ int cr_int8_convrot_gemm_ex(const void* X, const void* W, const void* xscale, co
  * cr_convrot_quant_int8_i8t: ck_convrot_quant_int8 (same codes and scales, the
  *   reference _int4/int4_gemm.hip:664-676 path) written in I8T; K <= cr_max_quant_bf6_k().
  * cr_int8_to_i8t: re-lays row-major int8 codes (a quantized weight) into I8T.
+ * cr_i8t_to_int8: the inverse of cr_int8_to_i8t on the first `rows` rows.
  * cr_int8_convrot_gemm_i8t: cr_int8_convrot_gemm_ex on I8T operands; the
  *   accumulators and outputs equal the row-major call's bit for bit.
  */
 int cr_convrot_quant_int8_i8t(const void* x, int in_dtype, void* qout, void* scaleout, int M, int K, int G,
                               void* stream);
 int cr_int8_to_i8t(const void* src, void* dst, int rows, int K, void* stream);
+int cr_i8t_to_int8(const void* src, void* dst, int rows, int K, void* stream);
 int cr_int8_convrot_gemm_i8t(const void* X, const void* W, const void* xscale, const void* wscale,
                              const void* bias, void* out, int M, int N, int K, int epilogue, void* stream);
 

@@ -2,6 +2,7 @@
 declares, the host-side API validates like the reference, the codec and the
 Linear replacement's load-time dispatch logic (with a fake comfy package)."""
 import ctypes
+import importlib
 import os
 import re
 import sys
@@ -91,9 +92,9 @@ def test_load_refuses_other_abi_version(native, monkeypatch):
 
 def test_library_queries_without_gpu(native):
     lib = native.load_library()
-    assert lib.cr_abi_version() == native.ABI_VERSION == 9
+    assert lib.cr_abi_version() == native.ABI_VERSION == 10
     assert lib.cr_max_quant_k() == 32768
-    assert lib.cr_max_quant_bf6_k() == 12288
+    assert lib.cr_max_quant_bf6_k() == 32768
 
 
 def test_argument_errors_return_minus_one(native):
@@ -127,8 +128,9 @@ def test_argument_errors_return_minus_one(native):
     assert lib.cr_int4_convrot_gemm_lora(n, n, n, n, n, n, n, 32, f, n, 4, 4, 64, 0, n) == -1  # null t/U
     assert lib.cr_int4_convrot_gemm_lora(n, n, n, n, n, n, n, 64, f, n, 4, 4, 48, 0, n) == -1  # K % 32
     assert lib.cr_convrot_quant_bf6(n, 1, n, n, 4, 192, 64, n) == -1          # K % 128
-    assert lib.cr_convrot_quant_bf6(n, 1, n, n, 4, 16384, 256, n) == -1       # above the bf6 quantizer's K
+    assert lib.cr_convrot_quant_bf6(n, 1, n, n, 4, 33024, 256, n) == -1       # above the bf6 quantizer's K
     assert lib.cr_int4_to_bf6(n, n, 4, 96, n) == -1                           # K % 128
+    assert lib.cr_bf6_to_int4(n, n, 4, 96, n) == -1                           # K % 128
     assert lib.cr_int4_convrot_gemm_bf6(n, n, n, n, n, n, 4, 4, 192, 0, n) == -1
     assert lib.cr_int4_convrot_gemm_bf6(n, n, n, n, n, n, 4, 4, 256, 4, n) == -1
     assert lib.ck_convrot_quant_int8(n, 1, n, n, 4, 256, 32, n) == -1      # bad G
@@ -138,8 +140,9 @@ def test_argument_errors_return_minus_one(native):
     assert lib.ck_int8_convrot_gemm(n, n, n, n, n, n, 4, 4, 64, 2, n) == -1  # out dtype
     assert lib.cr_int8_convrot_gemm_ex(n, n, n, n, n, n, 4, 4, 64, 2, n) == -1  # no eager bf16 chain for int8
     assert lib.cr_convrot_quant_int8_i8t(n, 1, n, n, 4, 160, 16, n) == -1      # K % 64
-    assert lib.cr_convrot_quant_int8_i8t(n, 1, n, n, 4, 16384, 256, n) == -1   # above the wave quantizer's K
+    assert lib.cr_convrot_quant_int8_i8t(n, 1, n, n, 4, 33024, 256, n) == -1   # above the row quantizer's K
     assert lib.cr_int8_to_i8t(n, n, 4, 96, n) == -1                             # K % 64
+    assert lib.cr_i8t_to_int8(n, n, 4, 96, n) == -1                             # K % 64
     assert lib.cr_int8_to_i8t(n, n, -1, 64, n) == -1                            # rows < 0
     assert lib.cr_int8_convrot_gemm_i8t(n, n, n, n, n, n, 4, 4, 96, 1, n) == -1  # K % 64
     assert lib.cr_int8_convrot_gemm_i8t(n, n, n, n, n, n, 4, 4, 64, 2, n) == -1  # no eager bf16 chain
@@ -369,3 +372,44 @@ def test_workspace_cache_reuses_grows_and_is_bounded(monkeypatch):
     assert len(native._workspaces) == native._MAX_WORKSPACES
     assert (None, 1) not in native._workspaces and (None, 2) not in native._workspaces
     assert (None, 2 + native._MAX_WORKSPACES) in native._workspaces
+
+
+def test_too_wide_rows_stay_bf16(ops_mod, backend):
+    """in_features above the fused quantizer's 32768: the API raises a
+    ValueError with the reason before any device work, a float layer is not
+    quantized (logged), and a prequantized int4 or int8 layer loads dequantized
+    in bf16 from its stored codes (the reference rotates such rows with torch,
+    _int4/__init__.py:59-66)."""
+    import logging
+    K = 33024                                      # 129 groups of 256
+    assert backend.max_quant_k() == 32768
+    with pytest.raises(ValueError, match="exceeds 32768"):
+        backend.quantize_convrot_w4a4_weight(torch.zeros(4, K))
+    with pytest.raises(ValueError, match="exceeds 32768"):
+        backend.convrot_w4a4_linear(torch.zeros(2, K), torch.zeros(4, K // 2, dtype=torch.int8), torch.ones(4))
+    with pytest.raises(ValueError, match="exceeds 32768"):
+        backend.convrot_w8a8_linear(torch.zeros(2, K), torch.zeros(4, K, dtype=torch.int8), torch.ones(4))
+    Ops = ops_mod.Int4ConvRotOps
+    lin = Ops.Linear(K, 4, bias=False)
+    assert not lin._should_quantize("x.", torch.zeros(4, K))
+    records = []
+    handler = logging.Handler()
+    handler.emit = records.append
+    logging.getLogger().addHandler(handler)
+    try:
+        lin._load_from_state_dict({"x.weight": torch.ones(4, K, dtype=torch.bfloat16)}, "x.", {}, True, [], [], [])
+        assert lin._qmode is None and bool((lin.weight == 1).all())      # a plain layer (the stand-in keeps f32)
+        assert any("exceeds 32768" in r.getMessage() for r in records)
+        g = torch.Generator().manual_seed(5)
+        for mode, cols in (("int4", K // 2), ("int8", K)):
+            q = torch.randint(-100, 100, (4, cols), generator=g, dtype=torch.int8)
+            s = torch.rand(4, generator=g) * 0.01 + 0.001
+            pre = Ops.Linear(K, 4, bias=False)
+            pre._load_from_state_dict({"p.weight": q, "p.weight_scale": s}, "p.", {}, True, [], [], [])
+            assert pre._qmode is None and pre._q is None, mode
+            deq = (backend.dequantize_convrot_w4a4_weight(q, s, 256) if mode == "int4" else
+                   importlib.import_module(backend.__name__ + ".int8_eager").dequantize_convrot_w8a8_weight(q, s, 256))
+            assert torch.equal(pre.weight.data, deq.to(torch.bfloat16).to(pre.weight.dtype)), mode
+        assert any("loading it dequantized" in r.getMessage() for r in records)
+    finally:
+        logging.getLogger().removeHandler(handler)

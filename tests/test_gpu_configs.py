@@ -170,8 +170,12 @@ def test_config4_token_sweep(native, oracle, gpu, M, K, N):
     a6, w6 = native.int4_to_bf6(xp), native.int4_to_bf6(wp)
     acc = native.int4_gemm_acc_bf6(a6, w6, M, N)
     # exact fp32 GEMM of the codes: every partial sum is an integer below 2^24
-    torch.backends.cuda.matmul.allow_tf32 = False
-    ref = (unpack_codes(xp) @ unpack_codes(wp).T).to(torch.int32)
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False     # restored below: later tests keep their setting
+    try:
+        ref = (unpack_codes(xp) @ unpack_codes(wp).T).to(torch.int32)
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev
     assert torch.equal(acc, ref)
     del ref
     out = native.int4_convrot_gemm_bf6(a6, w6, xs, ws, b, native.EPI_BF16)

@@ -45,8 +45,12 @@ def test_acc_bitexact_large(native, oracle, gpu, M, N, K):
     acc = native.int4_gemm_acc(xg, wg)
     unpack = lambda p: torch.stack([(p.to(torch.int32) << 28) >> 28, (p.to(torch.int32) << 24) >> 28],
                                    -1).reshape(p.shape[0], -1).float()
-    torch.backends.cuda.matmul.allow_tf32 = False
-    ref = (unpack(xg) @ unpack(wg).T).to(torch.int32)
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False     # restored below: later tests keep their setting
+    try:
+        ref = (unpack(xg) @ unpack(wg).T).to(torch.int32)
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev
     assert torch.equal(acc, ref)
     rows = np.random.RandomState(1).choice(M, 8, replace=False)
     assert np.array_equal(acc.cpu().numpy()[rows], oracle.int_gemm(xp[rows], wp))

@@ -87,11 +87,16 @@ def test_stochastic_weight_rounding(native, oracle, goldens, gpu):
     assert np.array_equal(s.cpu().numpy(), goldens["stoch_s"])
 
 
-def test_full_size_sampled_rows(native, oracle, gpu):
-    """16384 x 12288 heavy-tailed activations: every row is independent, so a
-    sample of rows checked against the oracle pins the full-size launch."""
-    M, K = 16384, 12288
-    x = outlier_activations(M, K, seed=123, student_t=True)
+@pytest.mark.parametrize("K", [3072, 12288])
+def test_full_size_sampled_rows(native, oracle, gpu, K):
+    """The rotate+quant configuration at full size, 16384 x {3072, 12288}
+    heavy-tailed (Student-t outlier channel) activations: every row is
+    independent, so a sample of rows checked against the oracle pins the
+    full-size launch.  The B6T output the linear uses decodes to the packed
+    codes on every row, and its scales are the same."""
+    M = 16384
+    print(f"rotquant full size {M}x{K} Student-t", flush=True)
+    x = outlier_activations(M, K, seed=123 + K, student_t=True)
     xg = x.cuda()
     q, s = native.convrot_quant_int4(xg, 256)
     q2, s2 = native.convrot_quant_int4(xg, 256)
@@ -107,6 +112,9 @@ def test_full_size_sampled_rows(native, oracle, gpu):
     codes = torch.stack([(q.to(torch.int32) << 28) >> 28, (q.to(torch.int32) << 24) >> 28], -1)
     assert int(codes.abs().max()) == 7
     assert bool((codes.abs().amax(dim=(1, 2)) == 7).all())
+    a6, s6 = native.convrot_quant_bf6(xg, 256)
+    assert torch.equal(s6, s)
+    assert torch.equal(native.bf6_to_int4(a6, M, K), q)
 
 
 @pytest.mark.parametrize("M,K", [(20000, 3072), (9000, 5120), (16500, 256)])

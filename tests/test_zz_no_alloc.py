@@ -82,3 +82,33 @@ def test_noalloc_refuses_shapes_beyond_the_scratch(native, gpu):
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     assert lib.cr_convrot_w4a4_linear_bf6_noalloc(n, 1, n, n, n, 0, n, n, 0, ctypes.c_float(1.0), n, 1, M, N, K, 256,
                                                   s) == -1
+
+
+def test_noalloc_replays_from_a_captured_graph(backend, native, gpu):
+    """After one call on the device (which looks up the scratch's address and
+    sets the kernels' LDS limits, neither of them a stream operation), the
+    entry point records into a HIP graph: every replay, with other calls on the
+    same scratch in between, gives the workspace entry point's bits."""
+    lib = native.load_library()
+    M, N, K, R = 1024, 3072, 3072, 32
+    print(f"noalloc graph capture: M={M} N={N} K={K} R={R}", flush=True)
+    args = operands(backend, M, N, K, R, seed=200)
+    ref = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    assert workspace_call(lib, *args, R, ref, M, N, K) == 0
+    out = torch.empty_like(ref)
+    assert noalloc(lib, *args, R, out, M, N, K) == 0          # the first call on this device, before capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = noalloc(lib, *args, R, out, M, N, K)
+    assert rc == 0
+    other = operands(backend, 300, 640, 3840, 0, seed=201)
+    other_out = torch.empty((300, 640), dtype=torch.bfloat16, device="cuda")
+    for i in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), i
+        # an eager call of another shape overwrites the scratch before the next replay
+        assert noalloc(lib, *other, 0, other_out, 300, 640, 3840) == 0
+        torch.cuda.synchronize()
