@@ -278,11 +278,10 @@ __global__ __launch_bounds__(kMaxThreads) void rotquant_kernel(
 // ---------------------------------------------------------------------------
 // Row-split kernel (K <= 32768).
 //
-// A workgroup of W waves quantizes one row at a time and walks rows
-// persistently (blockIdx.x, + gridDim.x, ...).  A row of K elements is K/16
-// chunks; wave w of the workgroup rotates chunks (p * W + w) * 64 + lane for
-// the passes p < P, so W * P passes of 64 lanes cover the row.  While a row is
-// rotated, every wave already loads its chunks of the workgroup's next row.
+// A workgroup of W waves quantizes row blockIdx.x (the grid is M).  A row of K
+// elements is K/16 chunks; wave w of the workgroup rotates chunks
+// (p * W + w) * 64 + lane for the passes p < P, so W * P passes of 64 lanes
+// cover the row.  While a pass is rotated, the wave loads its next pass.
 // The fp64 transpose and the code gather use a private LDS region per wave;
 // the row absmax is a shuffle reduction within each wave and then a max over
 // the W waves through LDS, the workgroup's one barrier per row.  Rounded
@@ -494,8 +493,13 @@ __device__ __forceinline__ float fmax3(float a, float b, float c) {
 // after the row's codes, so the loads' latency hides behind the rotation.
 // MAXW: the largest workgroup (in waves) the instance serves; RS = 8 or 16
 // row-absmax slots per row parity.
+// The kernel needs about 64 VGPRs, so the compiler would schedule for 8 waves
+// per SIMD; its 8.7 KB of LDS per wave admits at most 18 waves per CU (4 to 5
+// per SIMD), and scheduling for that occupancy leaves the loads more room
+// (interleaved A/B on MI355X, B6T out: 16384 x 3072 42.0 -> 37.4 us, 4608 x
+// 3072 13.8 -> 13.7 us).
 template <int DT, int G, int P, int OUT, bool LR, int MAXW = kRowMaxWaves>
-__global__ __launch_bounds__(64 * MAXW) void rotquant_row_kernel(
+__global__ __launch_bounds__(64 * MAXW) __attribute__((amdgpu_waves_per_eu(4, 5))) void rotquant_row_kernel(
         const void* __restrict__ x, int8_t* __restrict__ qout, float* __restrict__ sout, int M, int K,
         LoraSum ls) {
     constexpr int LPG = G / kChunk;
@@ -532,22 +536,22 @@ __global__ __launch_bounds__(64 * MAXW) void rotquant_row_kernel(
     const float kMagic = 12582912.0f;
     if (wv == 0 && lane < 2 * RS && (lane & (RS - 1)) >= W) red[lane] = 0.0f;   // before the first barrier
 
-    // One chunk buffer, loaded one pass ahead: while pass p is rotated, the
-    // wave already loads its next live pass of the row, or its first pass of
-    // the workgroup's next row (none after the workgroup's last row).  Lane
-    // loads are unconditional within a wave (a lane past the row end reads the
-    // pass's first chunk), so the load overwrites the buffer it was just
-    // converted from without a merge of old and new values.  The kernel walks
-    // rows row, row + gridDim.x, ..., so any grid up to M works.
-    ChunkRegs<DT> buf;
-    int row = blockIdx.x;     // < M: the grid never exceeds M
+    // One row per workgroup (the grid is M).  Two chunk buffers in turn: while
+    // pass p is rotated from bufs[p & 1], the wave loads its next pass into the
+    // other one, so no register copies carry a prefetch across passes.  Every
+    // load is unconditional (a lane past the row end reads the pass's first
+    // chunk, a next pass past the row end re-reads this one): with no branch
+    // around it, each pass waits for its own loads only.  Lanes past the row
+    // end (whole convrot groups, since K % G == 0) rotate those copies; they
+    // are left out of the row absmax and store no codes.
+    ChunkRegs<DT> bufs[2];
+    const int row = blockIdx.x;
     {
         const int c0 = wv * 64;   // < nchunks: W <= number of passes of a row
-        load_regs<DT>(x, (size_t)row * K + (size_t)(c0 + lane < nchunks ? c0 + lane : c0) * kChunk, buf);
+        load_regs<DT>(x, (size_t)row * K + (size_t)(c0 + lane < nchunks ? c0 + lane : c0) * kChunk, bufs[0]);
     }
 
-    for (int it = 0; row < M; row += gridDim.x, ++it) {
-        const int nrow = row + gridDim.x < M ? row + gridDim.x : row;
+    {
         Held<DT> hv[P];
         float lmax = 0.0f;
         float lp[8];                 // LoRA partials of rank column `lane` (LR, wave 0)
@@ -564,27 +568,25 @@ __global__ __launch_bounds__(64 * MAXW) void rotquant_row_kernel(
             if (c0 < nchunks) {
                 const int c = c0 + lane;
                 const bool ok = c < nchunks;
-                if ((nchunks & 63) && !ok) buf = ChunkRegs<DT>{};   // ragged last pass: zeros
                 double v[16];
-                regs_to_f64<DT>(buf, v);
-                {   // prefetch
+                regs_to_f64<DT>(bufs[p & 1], v);
+                if (p + 1 < P) {
                     const int n0 = ((p + 1) * W + wv) * 64;
-                    const bool same = p + 1 < P && n0 < nchunks;
-                    const int lr = same ? row : nrow;
-                    const int l0 = same ? n0 : wv * 64;
-                    if (same || nrow != row)   // wave-uniform: the workgroup's last row has no next pass to load
-                        load_regs<DT>(x, (size_t)lr * K + (size_t)(l0 + lane < nchunks ? l0 + lane : l0) * kChunk,
-                                      buf);
+                    const int l0 = n0 < nchunks ? n0 : c0;
+                    load_regs<DT>(x, (size_t)row * K + (size_t)(l0 + lane < nchunks ? l0 + lane : l0) * kChunk,
+                                  bufs[(p + 1) & 1]);
                 }
                 rotate_chunk<G>(v, tbuf, lane, gl, gfirst);
-                hold_chunk<DT>(v, hv[p], lmax);
+                float pmax = 0.0f;
+                hold_chunk<DT>(v, hv[p], pmax);
+                lmax = ok ? fmaxf(lmax, pmax) : lmax;
             }
         }
         // row absmax: across the wave (lmax is never NaN: it starts at 0 and
         // v_max3 drops NaN operands), then across the W waves
         lmax = wave_max_nonneg(lmax);
         if (W > 1) {
-            float* rb = red + (it & 1) * RS;
+            float* rb = red;
             if (lane == 0) rb[wv] = lmax;
             __syncthreads();
             const float4 r0 = reinterpret_cast<const float4*>(rb)[0];
@@ -605,12 +607,25 @@ __global__ __launch_bounds__(64 * MAXW) void rotquant_row_kernel(
         // multiple of 2 above it is not); fl32(a / QMAX) and a * fl32(1 / QMAX),
         // both within 2^-23 of a / QMAX, round to the same DT value.
         const float s = DT == DT_F32 ? a / QMAX : round_to_dt<DT>(a * (1.0f / QMAX));
-        if (wv == 0 && lane == 0) sout[row] = s;
         // bf16: v_rcp_f32 is within 1 ulp of 1 / s, so xr * rinv32 stays within
         // 2^-22 of xr / s, inside the 2^-17 the quotient keeps from every bf16
         // midpoint (file header)
         const float rinv32 = __builtin_amdgcn_rcpf(s);
         const double rinv = 1.0 / (double)s;
+        // B6T: the codes of flush f (after passes 2f, 2f+1) stay in registers
+        // until every flush of the row is converted, then all are stored: a
+        // store issued mid-loop would hold back the next flush, whose registers
+        // reuse the pending store's data (the wait covers every store in flight).
+        constexpr int NF = B6 ? (P + 1) / 2 : 1;
+        uint32_t fd[NF][6];
+        int fcg[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f) fcg[f] = -1;
+        // the other layouts: each pass's 16 code bytes (int8) or 8 packed bytes, and its chunk (-1: none)
+        uint32_t pw[P][4] = {};
+        int pc[P];
+#pragma unroll
+        for (int p2 = 0; p2 < P; ++p2) pc[p2] = -1;
 
 #pragma unroll
         for (int p = 0; p < P; ++p) {
@@ -682,35 +697,65 @@ __global__ __launch_bounds__(64 * MAXW) void rotquant_row_kernel(
                         const v16u words = {gq[0].x, gq[0].y, gq[0].z, gq[0].w, gq[1].x, gq[1].y, gq[1].z, gq[1].w,
                                             gq[2].x, gq[2].y, gq[2].z, gq[2].w, gq[3].x, gq[3].y, gq[3].z, gq[3].w};
                         const v6u r = __builtin_amdgcn_cvt_scalef32_pk32_bf6_bf16(__builtin_bit_cast(v32bf, words), 1.0f);
-                        const uint32_t d[6] = {r[0], r[1], r[2], r[3], r[4], r[5]};
-                        b6_store_group(qout, row, K, cg * kChunk, d);
+#pragma unroll
+                        for (int i = 0; i < 6; ++i) fd[p >> 1][i] = r[i];
                     }
+                    fcg[p >> 1] = live ? cg : -1;
                 }
                 continue;
             }
             wave_sync();
             const uint4 w = reinterpret_cast<const uint4*>(cb)[lane];
             wave_sync();
-            if (OUT == OUT_I8 && ok) {
-                *reinterpret_cast<uint4*>(qout + (size_t)row * K + (size_t)c * kChunk) = w;
-            } else if (OUT == OUT_I8T && ok) {
-                const int k0 = c * kChunk;
-                int8_t* chunk = qout + ((size_t)(row >> 8) * (K >> 6) + (k0 >> 6)) * I8T_CHUNK;
-                *reinterpret_cast<uint4*>(chunk + i8t_off(row & 255, (k0 >> 4) & 3)) = w;
-            } else if (ok) {
-                const uint32_t ws[4] = {w.x & 0x0f0f0f0fu, w.y & 0x0f0f0f0fu, w.z & 0x0f0f0f0fu,
-                                        w.w & 0x0f0f0f0fu};
-                uint32_t o[2];
+            if constexpr (!B6) {
+                if constexpr (OUT == OUT_PACK4) {
+                    const uint32_t ws[4] = {w.x & 0x0f0f0f0fu, w.y & 0x0f0f0f0fu, w.z & 0x0f0f0f0fu,
+                                            w.w & 0x0f0f0f0fu};
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const uint32_t t0 = ws[2 * h] | (ws[2 * h] >> 4);
-                    const uint32_t t1 = ws[2 * h + 1] | (ws[2 * h + 1] >> 4);
-                    o[h] = (t0 & 0xffu) | ((t0 >> 8) & 0xff00u) | ((t1 & 0xffu) << 16) | ((t1 << 8) & 0xff000000u);
+                    for (int h = 0; h < 2; ++h) {
+                        const uint32_t t0 = ws[2 * h] | (ws[2 * h] >> 4);
+                        const uint32_t t1 = ws[2 * h + 1] | (ws[2 * h + 1] >> 4);
+                        pw[p][h] = (t0 & 0xffu) | ((t0 >> 8) & 0xff00u) | ((t1 & 0xffu) << 16) |
+                                   ((t1 << 8) & 0xff000000u);
+                    }
+                } else {
+                    pw[p][0] = w.x; pw[p][1] = w.y; pw[p][2] = w.z; pw[p][3] = w.w;
                 }
-                *reinterpret_cast<uint2*>(qout + (size_t)row * (K / 2) + (size_t)c * (kChunk / 2)) =
-                    make_uint2(o[0], o[1]);
+                pc[p] = ok ? c : -1;
             }
         }
+        // Every store of the row goes out here, after the last LDS read: the
+        // stores' data registers stay live until all are issued (the asm below),
+        // so no wait for a store in flight holds back the row's other work.
+        if constexpr (B6) {
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+                if (fcg[f] >= 0) b6_store_group(qout, row, K, fcg[f] * kChunk, fd[f]);
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+                asm volatile("" :: "v"(fd[f][0]), "v"(fd[f][1]), "v"(fd[f][2]), "v"(fd[f][3]), "v"(fd[f][4]),
+                             "v"(fd[f][5]));
+        } else {
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                if (pc[p] < 0) continue;
+                const int k0 = pc[p] * kChunk;
+                if constexpr (OUT == OUT_I8) {
+                    *reinterpret_cast<uint4*>(qout + (size_t)row * K + k0) =
+                        make_uint4(pw[p][0], pw[p][1], pw[p][2], pw[p][3]);
+                } else if constexpr (OUT == OUT_I8T) {
+                    int8_t* chunk = qout + ((size_t)(row >> 8) * (K >> 6) + (k0 >> 6)) * I8T_CHUNK;
+                    *reinterpret_cast<uint4*>(chunk + i8t_off(row & 255, (k0 >> 4) & 3)) =
+                        make_uint4(pw[p][0], pw[p][1], pw[p][2], pw[p][3]);
+                } else {
+                    *reinterpret_cast<uint2*>(qout + (size_t)row * (K / 2) + k0 / 2) = make_uint2(pw[p][0], pw[p][1]);
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < P; ++p)
+                asm volatile("" :: "v"(pw[p][0]), "v"(pw[p][1]), "v"(pw[p][2]), "v"(pw[p][3]));
+        }
+        if (wv == 0 && lane == 0) sout[row] = s;
         if constexpr (LR) {
             // t = bf16(part[0] + .. + part[S-1]), the order of lora_reduce_kernel
             if (wv == 0) {
