@@ -192,3 +192,42 @@ def test_ops_forward_fused_and_side_path(backend, gpu):
     assert err < 1e-2, float(err)
     lora_part = (plain.h(x, y0) + other.h(x, y0)).double()
     assert ((y.double() - y0.double()) - lora_part).norm() / lora_part.norm() < 3e-2
+
+
+@pytest.mark.parametrize("M,N,K,R", [(512, 3072, 3072, 32), (300, 1024, 12288, 64)])
+def test_fused_lora_precision_vs_fp16_adapters(backend, native, gpu, M, N, K, R):
+    """The fused side path rounds D, U * scale and t to bf16 (8 significant
+    bits); the reference arms its adapters in fp16 (11 bits, int4_ops.py:
+    165-168) and ComfyUI's h() computes from those (its rounding is not
+    vendored).  Measured here: the fused LoRA term (f32 epilogue, with and
+    without the adapter) against the fp64 closed form of the fp16 adapters,
+    scale * (x @ D16^T) @ U16^T.  The bf16 roundings bound the error of each
+    term by about 3 * 2^-9 of the magnitudes involved; the test holds the
+    elementwise bound and reports the Frobenius error (below 1e-2 relative to
+    the LoRA term, about 1e-3 of a typical LoRA term's own size per rounding)."""
+    print(f"fused LoRA precision M={M} N={N} K={K} R={R}", flush=True)
+    rs = np.random.RandomState(M + R)
+    x = outlier_activations(M, K, seed=M + 1)
+    qw, ws = backend.quantize_convrot_w4a4_weight(normal_weight(N, K, seed=N).cuda())
+    w6 = backend.prepare_convrot_w4a4_weight_bf6(qw)
+    down16 = torch.from_numpy((rs.standard_normal((R, K)) * 0.02).astype(np.float32)).to(torch.float16)
+    up16 = torch.from_numpy((rs.standard_normal((N, R)) * 0.1).astype(np.float32)).to(torch.float16)
+    scale = 0.8 * 16.0 / R                                   # strength * alpha / rank
+    D, U = backend.fuse_lora_pairs([(down16.cuda(), up16.cuda(), scale)])
+    xg = x.cuda()
+    y_l = native.convrot_w4a4_linear_bf6(xg, w6, ws, None, D, U, 1.0, native.EPI_F32, 256, N)
+    y_0 = native.convrot_w4a4_linear_bf6(xg, w6, ws, None, None, None, 1.0, native.EPI_F32, 256, N)
+    ours = y_l.double().cpu().numpy() - y_0.double().cpu().numpy()
+    xd = x.double().numpy()
+    d16, u16 = down16.double().numpy(), up16.double().numpy()
+    ref = scale * (xd @ d16.T) @ u16.T
+    mag = scale * (np.abs(xd) @ np.abs(d16).T) @ np.abs(u16).T
+    err = np.abs(ours - ref)
+    # D, U*scale, t rounded to bf16 (2^-9 each), fp32 sums, and the f32 rounding of the two outputs
+    ulp_y = np.spacing(np.maximum(np.abs(y_l.double().cpu().numpy()), np.abs(y_0.double().cpu().numpy())).astype(
+        np.float32)).astype(np.float64)
+    bound = 3.2 * 2.0 ** -9 * mag + 2 * ulp_y
+    assert np.all(err <= bound), float((err / bound).max())
+    rel = float(np.linalg.norm(ours - ref) / np.linalg.norm(ref))
+    print(f"  relative Frobenius error of the fused LoRA term vs the fp16 closed form: {rel:.2e}", flush=True)
+    assert rel < 1e-2
