@@ -264,9 +264,18 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
         if (t == 4) read_one(st, s2, 3, f);
     };
     // DMA instruction j of block kb (past the end: a repeat of the last block)
+    // Tile rounds on an XCD (workgroup b runs on XCD b % 8, whose 32 CUs take
+    // its workgroups b / 8 = 0..31, 32..63, ... in rounds) alternate the
+    // direction of their k walk: a tile of an odd round starts with the k
+    // blocks the previous round ended with, whose chunks of the row panels the
+    // two rounds share are still in that XCD's L2.  Exact integer products: the
+    // sum is the same in any order.  Interleaved A/B on MI355X, M = 4608: qkv
+    // 85.6 -> 84.7 us, mlp_up 114.0 -> 111.3 us, one-round shapes unchanged.
+    const bool krev = !SPLIT && ((blockIdx.x >> 3) / 32 & 1);
     auto dma_one = [&](int kb, int j) __attribute__((always_inline)) {
         const uint32_t st = my_lds + (kb % B6_STAGES) * B6_STAGE_BYTES;
-        dma16(st + j * 1024, my_src + (size_t)min(kb, nkb - 1) * B6_CHUNK + j * 1024);
+        const int kc = min(kb, nkb - 1);
+        dma16(st + j * 1024, my_src + (size_t)(krev ? nkb - 1 - kc : kc) * B6_CHUNK + j * 1024);
     };
     // Rank-32 LoRA with a bf16 output: the epilogue's t rows m0 .. m0+255 and U
     // rows n0 .. n0+255 (64 bytes each, 32 KB in all, read once per workgroup
