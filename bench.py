@@ -95,13 +95,15 @@ def gpu_lead(torch, buf, fills=4):
         buf.fill_(0)
 
 
-def gemm_traffic_bytes():
-    """HBM bytes per bf6 GEMM launch (mean over the four linears) as measured by
-    the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this workload, scaled
-    by the 1 GiB copy calibration; None when that summary is absent."""
+def measured_traffic(key="traffic_bytes_per_launch"):
+    """HBM bytes per launch as measured by the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE runs of this workload, scaled by the 1 GiB copy calibration:
+    ``traffic_bytes_per_launch`` for the bf6 GEMM (mean over the four linears),
+    ``rotquant_traffic_bytes_per_launch`` for the B6T rotate+quant at
+    M=4608, K=3072.  None when that summary is absent."""
     try:
         for line in open(TRAFFIC_SUMMARY):
-            if line.startswith("traffic_bytes_per_launch:"):
+            if line.startswith(key + ":"):
                 return float(line.split(":", 1)[1])
     except OSError:
         pass
@@ -403,7 +405,7 @@ def main():
             "peak": PEAK_FP6_TFLOPS if args.path == "bf6" else PEAK_INT8_TOPS,
             "unit": "TFLOP/s",
             "frac": round(gemm_tops / (PEAK_FP6_TFLOPS if args.path == "bf6" else PEAK_INT8_TOPS), 4),
-            "traffic": gemm_traffic_bytes() if args.path == "bf6" else None,
+            "traffic": measured_traffic() if args.path == "bf6" else None,
         },
         "rotate_quant": {
             "kernel": {"bf6": "rotquant_row_kernel<bf16,256,3 passes,B6T out> (one wave per row)",
@@ -422,6 +424,7 @@ def main():
             "GBps_all_launches_step_events": round(rq_gbs, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
+            "traffic": measured_traffic("rotquant_traffic_bytes_per_launch") if args.path == "bf6" else None,
         },
         "gemm_TOPS": round(gemm_tops, 1),
         "gemm_pct_int8_peak": round(100 * gemm_tops / PEAK_INT8_TOPS, 2),
