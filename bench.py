@@ -95,6 +95,24 @@ def gpu_lead(torch, buf, fills=4):
         buf.fill_(0)
 
 
+def clock_ramp(torch, step, seconds):
+    """Untimed steps for about `seconds` of wall time (--clock-ramp-ms), before
+    the warmup steps the command line asks for.  The GPU leaves its idle clocks only after
+    some milliseconds of sustained load: on MI355X, 20 steps timed after 5
+    warmup steps (about 2 ms of work) ran 14% slower than after 50, so a short
+    warmup alone would time the clock ramp rather than the kernels.  Returns the
+    number of steps run (reported in the JSON line)."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            step()
+        n += 8
+        torch.cuda.synchronize()
+    return n
+
+
 def measured_traffic(key="traffic_bytes_per_launch"):
     """HBM bytes per launch as measured by the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE runs of this workload, scaled by the 1 GiB copy calibration:
@@ -153,6 +171,8 @@ def main():
     # 50 untimed steps (about 25 ms of load on the block linears) bring the GPU
     # to steady clocks: after 5, the next 20 steps still ran 14% slower
     ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--clock-ramp-ms", type=float, default=30.0,
+                    help="untimed steps for this long before the warmup steps (0: none)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="approximate CPU time for the oracle baseline (0 disables it)")
     ap.add_argument("--path", choices=("bf6", "int8", "w8a8"), default="bf6",
@@ -224,6 +244,7 @@ def main():
             if rc != 0:
                 raise RuntimeError(f"launch failed rc={rc}")
 
+    ramp_steps = clock_ramp(torch, step, args.clock_ramp_ms * 1e-3)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -382,6 +403,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_ramp_steps": ramp_steps,      # untimed, before the warmup (clock_ramp)
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
