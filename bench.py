@@ -565,7 +565,7 @@ def bench_gemm_sweep(args):
             out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
             ns = lib.cr_gemm_bf6_choose_nsplit(M, N, K)
             nb = lib.cr_gemm_bf6_splitk_workspace(M, N, ns)
-            wsp = torch.empty((max(nb, 16),), dtype=torch.uint8, device="cuda")
+            wsp = torch.zeros((max(nb, 2048),), dtype=torch.uint8, device="cuda")   # split counters start at 0
             call = (vp(a6.data_ptr()), vp(w6.data_ptr()), vp(xs.data_ptr()), vp(ws.data_ptr()), vp(b.data_ptr()),
                     None, None, 0, ctypes.c_float(0.0), vp(out.data_ptr()), M, N, K, 1, ns, vp(wsp.data_ptr()),
                     nb, sptr)
@@ -704,7 +704,7 @@ def bench_dit(args):
             out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
             b32 = m.bias.float().contiguous()
             nb = lib.cr_convrot_w4a4_linear_bf6_workspace(M, N, K, R)
-            wsp = torch.empty((max(nb, 16),), dtype=torch.uint8, device="cuda")
+            wsp = torch.zeros((max(nb, 2048),), dtype=torch.uint8, device="cuda")   # split counters start at 0
             keep += [x, out, b32, wsp]
             for kind, r in (("linear_lora", R), ("linear_plain", 0)):
                 calls.append((kind, lib.cr_convrot_w4a4_linear_bf6,

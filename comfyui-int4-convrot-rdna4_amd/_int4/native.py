@@ -30,7 +30,7 @@ _IN_DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 EPI_F32, EPI_BF16, EPI_BF16_EAGER, EPI_ACC = 0, 1, 2, 3
 
 # cr_abi_version() of the library these signatures describe
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _vp, _i = ctypes.c_void_p, ctypes.c_int
 _SIGNATURES = {
@@ -150,21 +150,33 @@ def _stream(device) -> int:
 # use) goes back to torch's allocator, which allocated it on that stream and
 # hands it out again only in that stream's order.  Calls captured into a HIP
 # graph get a buffer of their own.
+# The library keeps the split counters of its bf6 GEMM in the first
+# SPLIT_COUNTER_BYTES of every workspace: they must be zero when a buffer is
+# first used (every call leaves them zero), so a new buffer gets them cleared
+# by a fill kernel on the stream that will use it.
 _MAX_WORKSPACES = 16
+SPLIT_COUNTER_BYTES = 2048
 _workspaces: "collections.OrderedDict" = collections.OrderedDict()
 _workspaces_lock = threading.Lock()
+
+
+def _new_workspace(device, nbytes: int) -> torch.Tensor:
+    ws = torch.empty((max(nbytes, SPLIT_COUNTER_BYTES),), dtype=torch.uint8, device=device)
+    ws[:SPLIT_COUNTER_BYTES].zero_()
+    return ws
 
 
 def _workspace(device, stream: int, nbytes: int) -> torch.Tensor:
     if torch.cuda.is_current_stream_capturing():
         # a graph keeps the address it captured: give it a buffer of its own
-        # (from the graph's pool), never the stream's shared one
-        return torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=device)
+        # (from the graph's pool; its counters cleared inside the graph), never
+        # the stream's shared one
+        return _new_workspace(device, nbytes)
     key = (device.index, stream)
     with _workspaces_lock:
         ws = _workspaces.get(key)
         if ws is None or ws.numel() < nbytes:
-            ws = torch.empty((max(nbytes, 16),), dtype=torch.uint8, device=device)
+            ws = _new_workspace(device, nbytes)
             _workspaces[key] = ws
         _workspaces.move_to_end(key)
         while len(_workspaces) > _MAX_WORKSPACES:

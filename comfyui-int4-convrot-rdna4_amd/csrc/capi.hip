@@ -43,6 +43,11 @@ hipError_t gemm_splitk_launch(const int8_t* Xp, const int8_t* Wp, const float* x
 
 #define API extern "C" __attribute__((visibility("default")))
 
+// Bytes 0 .. 2047 of every workspace this library takes hold the split
+// counters of the bf6 GEMM: zero when a workspace is first used, and zero
+// again after every call (nothing else is ever written there).
+constexpr size_t kSplitCounterBytes = 2048;
+
 static int quant_args_ok(int in_dtype, int M, int K, int G) {
     if (!(G == 16 || G == 64 || G == 256)) return 0;
     if (M < 0 || K <= 0 || K % G != 0) return 0;
@@ -99,9 +104,11 @@ API int ck_int4_convrot_gemm_splitk(const void* Xp, const void* Wp, const void* 
 
 static int lora_rank_ok(int R) { return R >= 32 && R <= 128 && R % 32 == 0; }
 
+// the partials follow the counter region (untouched here)
 API size_t cr_lora_down_workspace(int M, int K, int R) {
     if (M <= 0 || K <= 0 || K % 16 != 0 || !lora_rank_ok(R)) return 0;
-    return convrot::lora_part_bytes(M, K, R);
+    const size_t need = convrot::lora_part_bytes(M, K, R);
+    return need > 0 ? kSplitCounterBytes + need : 0;
 }
 
 API int cr_lora_down(const void* x, int in_dtype, const void* D, void* t, int M, int K, int R, void* workspace,
@@ -109,9 +116,10 @@ API int cr_lora_down(const void* x, int in_dtype, const void* D, void* t, int M,
     if ((in_dtype != 1 && in_dtype != 2) || M < 0 || K <= 0 || K % 16 != 0 || !lora_rank_ok(R)) return -1;
     if (M == 0) return 0;
     const size_t need = convrot::lora_part_bytes(M, K, R);
-    if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return -1;
-    hipError_t e = convrot::lora_down_launch(x, in_dtype, D, t, M, K, R, reinterpret_cast<float*>(workspace),
-                                             reinterpret_cast<hipStream_t>(stream));
+    if (need > 0 && (workspace == nullptr || workspace_bytes < kSplitCounterBytes + need)) return -1;
+    float* part = need > 0 ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + kSplitCounterBytes)
+                           : nullptr;
+    hipError_t e = convrot::lora_down_launch(x, in_dtype, D, t, M, K, R, part, reinterpret_cast<hipStream_t>(stream));
     return (int)e;
 }
 
@@ -256,18 +264,23 @@ API int cr_int8_convrot_gemm_i8t(const void* X, const void* W, const void* xscal
 // epilogue and the LoRA term.  Intermediates live in the caller's workspace.
 // ---------------------------------------------------------------------------
 namespace {
-struct LinPlan { size_t a6, xs, t, lpart, part, total; int nsplit; };
+// Workspace layout: the GEMM's split region first (its counters at bytes
+// 0 .. 2047 of every workspace, whatever the shape and split, so that no
+// other intermediate of any call ever overwrites them), then the B6T codes,
+// the row scales, t and the LoRA partials.
+struct LinPlan { size_t part, a6, xs, t, lpart, total; int nsplit; };
 size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 LinPlan lin_plan(int M, int N, int K, int R) {
     LinPlan p{};
     const size_t rows = (size_t)((M + 255) / 256) * 256;
     p.nsplit = convrot::gemm_bf6_choose_nsplit(M, N, K);
-    p.a6 = 0;
-    p.xs = al256(rows * (size_t)K / 4 * 3);
+    p.part = 0;
+    const size_t split_bytes = convrot::gemm_bf6_splitk_workspace(M, N, p.nsplit);
+    p.a6 = al256(split_bytes > kSplitCounterBytes ? split_bytes : kSplitCounterBytes);
+    p.xs = p.a6 + al256(rows * (size_t)K / 4 * 3);
     p.t = p.xs + al256((size_t)M * 4);
     p.lpart = p.t + al256((size_t)M * R * 2);
-    p.part = p.lpart + (R > 0 ? al256(convrot::lora_part_bytes(M, K, R)) : 0);
-    p.total = p.part + convrot::gemm_bf6_splitk_workspace(M, N, p.nsplit);
+    p.total = p.lpart + (R > 0 ? al256(convrot::lora_part_bytes(M, K, R)) : 0);
     return p;
 }
 }  // namespace
@@ -371,4 +384,4 @@ API int cr_convrot_w4a4_linear_bf6_noalloc(const void* x, int in_dtype, const vo
 
 API int cr_max_quant_k(void) { return convrot::rotquant_max_k(); }
 
-API int cr_abi_version(void) { return 10; }
+API int cr_abi_version(void) { return 11; }

@@ -194,8 +194,8 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
     const int n0 = tn * B6_BN;
 
     float* sc = reinterpret_cast<float*>(lds6 + B6_RING_BYTES);
-    if constexpr (!SPLIT)
-        stage_scales(sc, xs, ws, bias, bias_dt, M, N, m0, n0, tid, B6_THREADS);   // visible after the loop's first barrier
+    ScaleRegs scr;                                            // staged in LDS after the main loop
+    if constexpr (!SPLIT) scr.load(xs, ws, bias, bias_dt, M, N, m0, n0, tid);
 
     // waves 0..3 copy the A chunk of a block, waves 4..7 the B chunk (6 KB each)
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -382,7 +382,8 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
         }
         return;
     }
-    __syncthreads();                                     // every wave is done with the stages
+    scr.store(sc, bias, bias_dt, M, N, m0, n0, tid);
+    __syncthreads();                                     // every wave is done with the stages; scales staged
     // keep the epilogue's index arithmetic out of the main loop's registers
     int em0 = m0, en0 = n0, elane = lane;
     asm volatile("" : "+s"(M), "+s"(N), "+v"(em0), "+v"(en0), "+v"(elane));
@@ -418,6 +419,17 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
 // by one DMA instruction (phase A: the second half of block kb+2, phase B: the
 // first half of block kb+3).  Same accumulators, same epilogue: the outputs
 // equal the 256 x 256 kernel's bit for bit.
+//
+// SPLIT (S = nsplit > 1): workgroup b takes tile b % T and the 128-k blocks
+// [s nkb / S, (s + 1) nkb / S) of split s = b / T.  Every workgroup stores its
+// raw accumulators (exact integers in fp32) in the workspace with device-scope
+// stores, waits until they are done and takes a ticket from the tile's
+// counter; the one that draws the last ticket adds the other S - 1 partials to
+// its own (exact in any order: integers below 2^24), sets the counter back to
+// zero and runs the epilogue.
+// No workgroup waits for another, so no launch order or residency can stall
+// the grid.  The counters (one per tile, at most 512) must be zero when a
+// workspace is first used; every call leaves them zero.
 // ---------------------------------------------------------------------------
 constexpr int B6S_BM = 128, B6S_BN = 128;
 constexpr int B6S_THREADS = 256;
@@ -428,13 +440,16 @@ constexpr int B6S_LOADS = B6S_STAGE_BYTES / 16 / B6S_THREADS;  // 6 DMA instruct
 static_assert(B6S_LOADS == 6, "three copies per phase");
 static_assert((B6S_STAGES - 2) * B6S_LOADS + B6S_LOADS / 2 <= 63, "vmcnt range");
 constexpr int B6S_RING_BYTES = B6S_STAGES * B6S_STAGE_BYTES;
-constexpr int B6S_LDS_BYTES = B6S_RING_BYTES + EPI_SCALE_FLOATS * 4;
+constexpr int B6S_LDS_BYTES = B6S_RING_BYTES + EPI_SCALE_FLOATS * 4 + 16;   // + the split ticket
+constexpr int B6S_MAX_SPLIT_TILES = 512;                        // split counters per workspace
+constexpr int B6S_PART_FLOATS = B6S_BM * B6S_BN;                // one tile's partial: 64 KB
 
-template <int EPI, int LR>
+template <int EPI, int LR, bool SPLIT>
 __global__ __launch_bounds__(B6S_THREADS) void w4a4_gemm_bf6_small_kernel(
         const uint8_t* __restrict__ A6, const uint8_t* __restrict__ W6,
         const float* __restrict__ xs, const float* __restrict__ ws, const void* __restrict__ bias, int bias_dt,
-        void* __restrict__ out, int M, int N, int K, LoraArgs lora, int gm) {
+        void* __restrict__ out, int M, int N, int K, LoraArgs lora, int gm, int nsplit,
+        float* __restrict__ part, unsigned* __restrict__ cnt) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds6[];
 
     const int tid = threadIdx.x;
@@ -442,20 +457,28 @@ __global__ __launch_bounds__(B6S_THREADS) void w4a4_gemm_bf6_small_kernel(
     const int wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int tiles_m = (M + B6S_BM - 1) / B6S_BM, tiles_n = (N + B6S_BN - 1) / B6S_BN;
-    const int nkb = K / 128;
-    int tm, tn;
-    tile_of_block(blockIdx.x, tiles_m, tiles_n, gm, tm, tn);
+    const int nkb_all = K / 128;
+    int tm, tn, kb0 = 0, nkb = nkb_all, split = 0, tix = blockIdx.x;
+    if constexpr (SPLIT) {
+        const int T = tiles_m * tiles_n;
+        split = blockIdx.x / T;
+        tix = blockIdx.x - split * T;
+        kb0 = (int)((long long)split * nkb_all / nsplit);
+        nkb = (int)((long long)(split + 1) * nkb_all / nsplit) - kb0;
+    }
+    tile_of_block(tix, tiles_m, tiles_n, gm, tm, tn);
     const int m0 = tm * B6S_BM;
     const int n0 = tn * B6S_BN;
 
     float* sc = reinterpret_cast<float*>(lds6 + B6S_RING_BYTES);
-    stage_scales(sc, xs, ws, bias, bias_dt, M, N, m0, n0, tid, B6S_THREADS);   // visible after the first barrier
+    ScaleRegs scr;                                              // staged in LDS after the main loop
+    scr.load(xs, ws, bias, bias_dt, M, N, m0, n0, tid);
 
     // copy j (0..5) of this wave is instruction w*6 + j of the stage's 24: 0..11
     // the A half (8 P KB, then 4 Q KB), 12..23 the B half
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    const uint8_t* a_chunks = A6 + (size_t)(m0 >> 8) * nkb * B6_CHUNK;
-    const uint8_t* b_chunks = W6 + (size_t)(n0 >> 8) * nkb * B6_CHUNK;
+    const uint8_t* a_chunks = A6 + ((size_t)(m0 >> 8) * nkb_all + kb0) * B6_CHUNK;
+    const uint8_t* b_chunks = W6 + ((size_t)(n0 >> 8) * nkb_all + kb0) * B6_CHUNK;
     const int a_half = (m0 >> 7) & 1, b_half = (n0 >> 7) & 1;
     auto dma_one = [&](int kb, int j) __attribute__((always_inline)) {
         const int ins = wave_u * B6S_LOADS + j;                    // wave-uniform, 0..23
@@ -560,6 +583,39 @@ __global__ __launch_bounds__(B6S_THREADS) void w4a4_gemm_bf6_small_kernel(
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));                 // the copies past the end have landed
     __syncthreads();                                          // every wave is done with the stages
+    if constexpr (SPLIT) {
+        // Partial of split s: value q (0..63) of a lane is acc[q / 32][(q / 16) % 2][q % 16], at
+        // part[((s T + tile) 4 + wave) 4096 + q 64 + lane].  Written and read with device-scope
+        // relaxed atomic accesses (coherent across the XCDs' L2 caches without writing an L2 back);
+        // each wave's vmcnt(0) before the barrier orders its stores before the ticket.
+        const int T = tiles_m * tiles_n;
+        auto slot = [&](int s) { return part + ((size_t)(s * T + tix) * 4 + wave) * 4096 + lane; };
+        float* dst = slot(split);
+#pragma unroll
+        for (int q = 0; q < 64; ++q)
+            __hip_atomic_store(dst + q * 64, acc[q >> 5][(q >> 4) & 1][q & 15], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));             // this wave's partial is stored
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __syncthreads();                                      // ... and every other wave's
+        unsigned* ticket = reinterpret_cast<unsigned*>(lds6 + B6S_RING_BYTES + EPI_SCALE_FLOATS * 4);
+        if (tid == 0) *ticket = __hip_atomic_fetch_add(cnt + tix, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (*ticket != (unsigned)nsplit - 1) return;          // another split finishes this tile
+        if (tid == 0) __hip_atomic_store(cnt + tix, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int s = 0; s < nsplit; ++s) {
+            if (s == split) continue;
+            const float* src = slot(s);
+            float p[64];
+#pragma unroll
+            for (int q = 0; q < 64; ++q) p[q] = __hip_atomic_load(src + q * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int q = 0; q < 64; ++q) acc[q >> 5][(q >> 4) & 1][q & 15] += p[q];
+        }
+    }
+    scr.store(sc, bias, bias_dt, M, N, m0, n0, tid);
+    __syncthreads();
     int em0 = m0, en0 = n0, elane = lane;
     asm volatile("" : "+s"(M), "+s"(N), "+v"(em0), "+v"(en0), "+v"(elane));
     constexpr int SCR = B6S_RING_BYTES / (B6S_THREADS / 64);
@@ -613,6 +669,11 @@ __global__ __launch_bounds__(64 * B6R_WAVES) void w4a4_bf6_splitk_reduce_kernel(
 
 bool gemm_bf6_small_tiles(int M, int N, int K);
 
+// Every split workspace starts with the counters of the quarter-tile kernel's
+// split (B6S_MAX_SPLIT_TILES of them); the partials follow.
+constexpr int BF6_SPLIT_COUNTER_BYTES = B6S_MAX_SPLIT_TILES * 4;
+static_assert(BF6_SPLIT_COUNTER_BYTES == 2048, "counter region of the documented workspace layout");
+
 template <int EPI, int LR>
 static hipError_t launch_bf6(const uint8_t* A6, const uint8_t* W6, const float* xs, const float* ws,
                              const void* bias, int bias_dt, void* out, int M, int N, int K, const LoraArgs& la,
@@ -622,15 +683,33 @@ static hipError_t launch_bf6(const uint8_t* A6, const uint8_t* W6, const float* 
     int dev = 0;
     hipError_t e = current_device(&dev);
     if (e != hipSuccess) return e;
-    if (nsplit <= 1 && gemm_bf6_small_tiles(M, N, K)) {
-        static std::atomic<bool> attr_small[kMaxDev];
-        e = lds_limit_once(attr_small, dev, reinterpret_cast<const void*>(&w4a4_gemm_bf6_small_kernel<EPI, LR>),
-                           B6S_LDS_BYTES);
-        if (e != hipSuccess) return e;
+    // workspace (nsplit > 1): the split counters, then the partials
+    unsigned* cnt = nullptr;
+    if (nsplit > 1) {
+        cnt = reinterpret_cast<unsigned*>(part);
+        part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(part) + BF6_SPLIT_COUNTER_BYTES);
+    }
+    if (gemm_bf6_small_tiles(M, N, K)) {
         const int sm = (M + B6S_BM - 1) / B6S_BM;
         const int sn = (N + B6S_BN - 1) / B6S_BN;
-        hipLaunchKernelGGL((w4a4_gemm_bf6_small_kernel<EPI, LR>), dim3(sm * sn), dim3(B6S_THREADS), B6S_LDS_BYTES, st,
-                           A6, W6, xs, ws, bias, bias_dt, out, M, N, K, la, tile_group_rows(sm));
+        if (nsplit <= 1) {
+            static std::atomic<bool> attr_small[kMaxDev];
+            e = lds_limit_once(attr_small, dev,
+                               reinterpret_cast<const void*>(&w4a4_gemm_bf6_small_kernel<EPI, LR, false>),
+                               B6S_LDS_BYTES);
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL((w4a4_gemm_bf6_small_kernel<EPI, LR, false>), dim3(sm * sn), dim3(B6S_THREADS),
+                               B6S_LDS_BYTES, st, A6, W6, xs, ws, bias, bias_dt, out, M, N, K, la,
+                               tile_group_rows(sm), 1, nullptr, nullptr);
+            return hipGetLastError();
+        }
+        static std::atomic<bool> attr_small_split[kMaxDev];
+        e = lds_limit_once(attr_small_split, dev,
+                           reinterpret_cast<const void*>(&w4a4_gemm_bf6_small_kernel<EPI, LR, true>), B6S_LDS_BYTES);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((w4a4_gemm_bf6_small_kernel<EPI, LR, true>), dim3(sm * sn * nsplit), dim3(B6S_THREADS),
+                           B6S_LDS_BYTES, st, A6, W6, xs, ws, bias, bias_dt, out, M, N, K, la, tile_group_rows(sm),
+                           nsplit, part, cnt);
         return hipGetLastError();
     }
     const int tiles_m = (M + B6_BM - 1) / B6_BM;
@@ -714,19 +793,42 @@ hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, cons
 // per (tile, split) partial (256 KB written and read back).  A split must win
 // by 8% to be taken.
 // The 128 x 128 kernel when its grid stays within about two workgroups per CU
-// and rows are short (long rows go faster through the k-split 256 x 256
-// kernel).  Measured against the 256 x 256 kernel with its chosen split (HIP
-// events, bf16 out): 512 x 3072 -> 3072 16.8 / 25.4 us, 1024 x 3072 -> 3072
-// 17.5 / 23.8, 2048 x 3072 -> 3072 23.5 / 26.3, 512 x 3072 -> 12288 22.0 /
-// 24.5, 512 x 3840 -> 15360 26.9 / 28.6; but 1024 x 3072 -> 9216 34.5 / 26.3
-// and 512 x 12288 -> 3072 41.1 / 32.2.
+// and rows are short, or the grid is small enough for the kernel's own split
+// (long rows on at most 192 quarter tiles); other long rows go through the
+// k-split 256 x 256 kernel.  Measured against the 256 x 256 kernel with its
+// chosen split (HIP events, bf16 out): 512 x 3072 -> 3072 16.8 / 25.4 us,
+// 1024 x 3072 -> 3072 17.5 / 23.8, 2048 x 3072 -> 3072 23.5 / 26.3, 512 x
+// 3072 -> 12288 22.0 / 24.5, 512 x 3840 -> 15360 26.9 / 28.6; but 1024 x
+// 3072 -> 9216 34.5 / 26.3 and, unsplit, 512 x 12288 -> 3072 41.1 / 32.2.
+// Burst-timed on MI355X with the quarter-tile split (below): 512 x 12288 ->
+// 3072 27.6 us (S = 2) against 30.0 for the 256 x 256 split and reduce, 1024 x
+// 12288 -> 3072 39.3 against 40.0; 2048 x 12288 -> 3072 63.8 unsplit against
+// 60.4, so 384 quarter tiles with long rows stay on the 256 x 256 kernel.
 bool gemm_bf6_small_tiles(int M, int N, int K) {
     const long long tiles = (long long)((M + B6S_BM - 1) / B6S_BM) * ((N + B6S_BN - 1) / B6S_BN);
-    return tiles <= 512 && K <= 4096;
+    return tiles <= B6S_MAX_SPLIT_TILES && (K <= 4096 || tiles <= 192);
+}
+
+// Splits of the quarter-tile kernel.  Its launch costs about 5.5 us however
+// short the rows (6.1 us at K = 256, M x N = 512 x 3072: the first copies'
+// latency, the epilogue and the store drain), a 128-k block 0.35 us with one
+// workgroup per CU, and two workgroups on a CU run each at about half speed;
+// the split's partial exchange (device-scope stores, the ticket, the last
+// split's loads) adds 4-5 us.  So a split pays only for long rows on a grid
+// that leaves CUs free: measured at 512 x K -> 3072 (96 tiles), K = 3072
+// 13.7 us unsplit / 13.9 split in two, K = 6144 22.0 / 18.5, K = 12288 38.9 /
+// 27.4 (S = 4: 27.5); 1024 x 12288 -> 3072 (192 tiles) 44.0 / 39.3; at
+// K = 3072 no split won on any of 15 shapes.
+static int small_nsplit(int M, int N, int K) {
+    const int T = ((M + B6S_BM - 1) / B6S_BM) * ((N + B6S_BN - 1) / B6S_BN);
+    const int nkb = K / 128;
+    if (nkb < 48) return 1;
+    if (T <= 64 && nkb >= 96) return 4;
+    return T <= 192 ? 2 : 1;
 }
 
 int gemm_bf6_choose_nsplit(int M, int N, int K) {
-    if (gemm_bf6_small_tiles(M, N, K)) return 1;
+    if (gemm_bf6_small_tiles(M, N, K)) return small_nsplit(M, N, K);
     const int tiles = ((M + B6_BM - 1) / B6_BM) * ((N + B6_BN - 1) / B6_BN);
     const int nkb = K / 128;
     auto cost = [&](int s) {
@@ -745,9 +847,15 @@ int gemm_bf6_choose_nsplit(int M, int N, int K) {
     return bc < 0.92 * c1 ? best : 1;
 }
 
+// The counters, then the larger of the two kernels' partials (a quarter-tile
+// grid has at most four times the tiles of the full-tile one, at a quarter of
+// the bytes each).
 size_t gemm_bf6_splitk_workspace(int M, int N, int nsplit) {
     const size_t tiles = (size_t)((M + B6_BM - 1) / B6_BM) * ((N + B6_BN - 1) / B6_BN);
-    return nsplit <= 1 ? 0 : (size_t)nsplit * tiles * 8 * 8192 * sizeof(float);
+    const size_t qtiles = (size_t)((M + B6S_BM - 1) / B6S_BM) * ((N + B6S_BN - 1) / B6S_BN);
+    const size_t full = (size_t)nsplit * tiles * 8 * 8192 * sizeof(float);
+    const size_t small = (size_t)nsplit * qtiles * B6S_PART_FLOATS * sizeof(float);
+    return nsplit <= 1 ? 0 : BF6_SPLIT_COUNTER_BYTES + (full > small ? full : small);
 }
 
 }  // namespace convrot

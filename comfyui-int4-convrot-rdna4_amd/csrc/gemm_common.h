@@ -74,6 +74,41 @@ __device__ __forceinline__ void stage_scales(float* sc, const float* __restrict_
     stage_scales(sc, xs, ws, static_cast<const void*>(bias), DT_F32, M, N, m0, n0, tid, nthreads);
 }
 
+// The same staging in two steps: load() issues the global loads into
+// registers at kernel start, ahead of the main loop's first copies, so their
+// latency overlaps the copies' instead of preceding them (stage_scales waits
+// for each load before its LDS store); store() writes them to LDS after the
+// main loop, whose final vmcnt(0) has retired them.  Threads 0..255 (whole
+// waves) each load the xs, ws and bias entries of tile row / column k = tid,
+// with clamped indices, so that no load is conditional on a lane and none
+// waits for another.
+struct ScaleRegs {
+    float x, w;
+    uint32_t b;   // the bias element's bits in its own type
+    __device__ __forceinline__ void load(const float* __restrict__ xs, const float* __restrict__ ws,
+                                         const void* __restrict__ bias, int bias_dt, int M, int N, int m0, int n0,
+                                         int tid) {
+        x = 0.0f; w = 0.0f; b = 0u;
+        if (tid >= 256) return;
+        const int kx = min(m0 + tid, M - 1), kw = min(n0 + tid, N - 1);
+        if (xs) x = xs[kx];
+        if (ws) w = ws[kw];
+        if (bias) b = bias_dt == DT_F32 ? __float_as_uint(reinterpret_cast<const float*>(bias)[kw])
+                                        : (uint32_t)reinterpret_cast<const uint16_t*>(bias)[kw];
+    }
+    // the values stage_scales writes (0 outside M / N, -0 for an absent bias)
+    __device__ __forceinline__ void store(float* sc, const void* __restrict__ bias, int bias_dt, int M, int N,
+                                          int m0, int n0, int tid) const {
+        if (tid >= 256) return;
+        sc[tid] = m0 + tid < M ? x : 0.0f;
+        sc[256 + tid] = n0 + tid < N ? w : 0.0f;
+        float v = -0.0f;
+        if (bias && n0 + tid < N)
+            v = bias_dt == DT_F16 ? f16bits_to_f32(b) : bias_dt == DT_BF16 ? __uint_as_float(b << 16) : __uint_as_float(b);
+        sc[512 + tid] = v;
+    }
+};
+
 // Epilogue of a wave's FMT x FNT grid of 32x32 accumulator tiles at (row0, col0).
 // 32x32 layout: lane l, register r -> col = l % 32, row = 8 (r / 4) + 4 (l / 32) + r % 4.
 // The LoRA product uses the same layout (bf16 MFMA over R), issued by the

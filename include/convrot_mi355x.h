@@ -21,6 +21,14 @@
  *     hipError_t of the launch (no device synchronisation).
  *   - packed int4 layout: int8 [rows, K/2], element 2j in the low nibble of
  *     byte j, 2j+1 in the high nibble (reference _int4/_codec.py:19-25).
+ *   - workspaces (cr_lora_down, cr_int4_convrot_gemm_bf6_splitk,
+ *     cr_convrot_w4a4_linear_bf6): bytes 0..2047 of every workspace hold the
+ *     split counters of the bf6 GEMM.  They must be zero when a workspace is
+ *     first used (clear them once after allocating it); every call leaves them
+ *     zero, and no call writes anything else there, so one workspace can serve
+ *     every entry point and shape in stream order.  The sizes returned by the
+ *     *_workspace queries include these 2048 bytes.  The no-allocation entry
+ *     point's static array starts zeroed and keeps the same rule.
  */
 #ifndef CONVROT_MI355X_H
 #define CONVROT_MI355X_H
@@ -109,8 +117,9 @@ int cr_convrot_quant_int4_stochastic(const void* x, int in_dtype, const void* no
  *   x [M, K] bf16 (in_dtype 1) or f16 (2), D [R, K] bf16, t [M, R] bf16;
  *   R in {32, 64, 96, 128}, K % 16 == 0.
  * Depending on the shape (never on the device) the projection is split over
- * k: f32 partial sums go to `workspace` (cr_lora_down_workspace(M, K, R)
- * bytes; 0 bytes, and workspace may be NULL, for an unsplit shape), then their
+ * k: f32 partial sums go to `workspace` after its counter region
+ * (cr_lora_down_workspace(M, K, R) bytes; 0 bytes, and workspace may be NULL,
+ * for an unsplit shape), then their
  * sum in split order is rounded once to bf16.  The linear
  * (cr_convrot_w4a4_linear_bf6) computes the same t bit for bit.
  * Together with cr_int4_convrot_gemm_lora it replaces the per-adapter
@@ -190,10 +199,13 @@ int cr_int4_convrot_gemm_bf6_lora(const void* A6, const void* W6, const void* xs
 
 /*
  * Split-K form of the bf6 GEMM for small tile grids (few rows, large K): S
- * workgroups per 256 x 256 output tile each take 1/S of the 128-k blocks and
- * store their raw accumulators (exact integers) in `workspace`; a second kernel
- * sums the S partials in a fixed order and runs the same epilogue code, so the
- * outputs are bit-identical to cr_int4_convrot_gemm_bf6 / _lora for every S.
+ * workgroups per output tile each take 1/S of the 128-k blocks and store their
+ * raw accumulators (exact integers) in `workspace`.  On grids of 128 x 128
+ * tiles the split that finishes last sums the S partials in the same kernel
+ * (a ticket from the tile's counter in the workspace's counter region decides
+ * which); on 256 x 256 tiles a second kernel sums them.  Integer partials sum
+ * exactly in any order, so the outputs are bit-identical to
+ * cr_int4_convrot_gemm_bf6 / _lora for every S.
  *   t == NULL: no LoRA term, epilogue 0..3; else LoRA as cr_int4_convrot_gemm_bf6_lora
  *   (epilogue 0..2).  1 <= nsplit <= K / 128; nsplit == 1 needs no workspace,
  *   otherwise workspace_bytes >= cr_gemm_bf6_splitk_workspace(M, N, nsplit).
@@ -208,11 +220,11 @@ int cr_int4_convrot_gemm_bf6_splitk(const void* A6, const void* W6, const void* 
                                     void* out, int M, int N, int K, int epilogue, int nsplit,
                                     void* workspace, size_t workspace_bytes, void* stream);
 
-/* The library's k-split count for an M x N x K bf6 GEMM (1 = no split; always
- * 1 for the grids that run on 128 x 128 tiles). */
+/* The library's k-split count for an M x N x K bf6 GEMM (1 = no split). */
 int cr_gemm_bf6_choose_nsplit(int M, int N, int K);
 
-/* Workspace bytes of cr_int4_convrot_gemm_bf6_splitk: nsplit * tiles * 256 KB (0 when nsplit == 1). */
+/* Workspace bytes of cr_int4_convrot_gemm_bf6_splitk: 2048 counter bytes plus
+ * nsplit * (256 x 256 tiles) * 256 KB (0 when nsplit == 1). */
 size_t cr_gemm_bf6_splitk_workspace(int M, int N, int nsplit);
 
 /*

@@ -92,7 +92,7 @@ def test_load_refuses_other_abi_version(native, monkeypatch):
 
 def test_library_queries_without_gpu(native):
     lib = native.load_library()
-    assert lib.cr_abi_version() == native.ABI_VERSION == 10
+    assert lib.cr_abi_version() == native.ABI_VERSION == 11
     assert lib.cr_max_quant_k() == 32768
     assert lib.cr_max_quant_bf6_k() == 32768
 
@@ -118,10 +118,11 @@ def test_argument_errors_return_minus_one(native):
     # the split plan, a function of the shape only: 64-row workgroups over 4 k
     # ranges for the image stream's long rows, 16-row ones over the whole of K
     # for its short rows (no partials), 16-row ones over 8 ranges for the text stream
-    assert lib.cr_lora_down_workspace(4096, 12288, 32) == 4 * 4096 * 32 * 4
+    # the split counter region (2 KB) leads every workspace
+    assert lib.cr_lora_down_workspace(4096, 12288, 32) == 2048 + 4 * 4096 * 32 * 4
     assert lib.cr_lora_down_workspace(4096, 3072, 32) == 0
-    assert lib.cr_lora_down_workspace(512, 3072, 32) == 8 * 512 * 32 * 4
-    assert lib.cr_lora_down_workspace(4608, 3072, 64) == 4 * 4608 * 64 * 4
+    assert lib.cr_lora_down_workspace(512, 3072, 32) == 2048 + 8 * 512 * 32 * 4
+    assert lib.cr_lora_down_workspace(4608, 3072, 64) == 2048 + 4 * 4608 * 64 * 4
     assert lib.cr_lora_down_workspace(64, 256, 32) == 0                    # K of one 256-k range: one split
     assert lib.cr_lora_down_workspace(4, 40, 32) == 0
     assert lib.cr_int4_convrot_gemm_lora(n, n, n, n, n, n, n, 32, f, n, 4, 4, 64, 3, n) == -1  # acc dump
@@ -290,15 +291,17 @@ def test_ops_refuses_unknown_prequant_layout(ops_mod):
 
 def test_split_choice_and_workspace(native):
     """The k-split choice is host arithmetic: large tile grids never split,
-    small-M / large-K products do, within 2 .. nkb; the workspace is S * tiles
-    * 256 KB."""
+    small-M / large-K products do, within 2 .. nkb; the workspace is the 2 KB
+    counter region plus S * tiles * 256 KB (the quarter-tile kernel's partials
+    never need more)."""
     lib = native.load_library()
     assert lib.cr_gemm_bf6_choose_nsplit(4608, 3072, 3072) == 1
     assert lib.cr_gemm_bf6_choose_nsplit(4608, 12288, 3072) == 1
     s = lib.cr_gemm_bf6_choose_nsplit(512, 3072, 12288)
     assert 2 <= s <= 96
     assert lib.cr_gemm_bf6_choose_nsplit(256, 256, 256) <= 2
-    assert lib.cr_gemm_bf6_splitk_workspace(512, 3072, 4) == 4 * 24 * 256 * 256 * 4
+    assert lib.cr_gemm_bf6_splitk_workspace(512, 3072, 4) == 2048 + 4 * 24 * 256 * 256 * 4
+    assert lib.cr_gemm_bf6_splitk_workspace(300, 300, 2) == 2048 + 2 * 4 * 256 * 256 * 4
     assert lib.cr_gemm_bf6_splitk_workspace(300, 300, 1) == 0
 
 
@@ -362,10 +365,11 @@ def test_workspace_cache_reuses_grows_and_is_bounded(monkeypatch):
     monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
     monkeypatch.setattr(native, "_workspaces", type(native._workspaces)())
     dev = torch.device("cpu")
-    a = native._workspace(dev, 1, 100)
+    a = native._workspace(dev, 1, 3000)
+    assert int(a[:native.SPLIT_COUNTER_BYTES].count_nonzero()) == 0      # split counters start at zero
     assert native._workspace(dev, 1, 50) is a
-    b = native._workspace(dev, 1, 200)
-    assert b is not a and b.numel() >= 200
+    b = native._workspace(dev, 1, 5000)
+    assert b is not a and b.numel() >= 5000
     assert native._workspace(dev, 2, 10) is not b
     for s in range(3, 3 + native._MAX_WORKSPACES):
         native._workspace(dev, s, 10)

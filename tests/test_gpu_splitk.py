@@ -22,8 +22,11 @@ def operands(native, M, N, K, seed):
     return xp, wp, native.int4_to_bf6(cu(xp)), native.int4_to_bf6(cu(wp)), cu(xs), cu(ws), cu(b)
 
 
+# Grids of at most 512 quarter tiles take the 128 x 128 kernel, whose splits
+# are reduced in the kernel by the last split of each tile; larger grids take
+# the 256 x 256 partial kernel and the reduce kernel (the last case).
 SPLIT_CASES = [(512, 3072, 12288, [2, 5, 6, 16, 96]), (300, 700, 1024, [2, 3, 8]), (1024, 3072, 3072, [2, 4, 24]),
-               (64, 256, 256, [2]), (257, 513, 3840, [7, 30])]
+               (64, 256, 256, [2]), (257, 513, 3840, [7, 30]), (640, 13312, 2048, [2, 4])]
 
 
 @pytest.mark.parametrize("M,N,K,splits", SPLIT_CASES)
@@ -78,3 +81,21 @@ def test_auto_split_linear_matches_unsplit(backend, native, gpu):
     y1 = native.int4_convrot_gemm_bf6(a6, backend.prepare_convrot_w4a4_weight_bf6(qw), xs, ws, b,
                                       native.EPI_BF16, nsplit=1)
     assert torch.equal(y, y1)
+
+
+def test_split_counters_left_zero(native, gpu):
+    """Every split call leaves the counter region of its workspace zero, also
+    across shapes and split counts sharing the stream's workspace, and a
+    second run of each split equals the first."""
+    st = native._stream(torch.device("cuda"))
+    first = {}
+    for M, N, K, s in [(512, 3072, 12288, 6), (300, 700, 1024, 3), (512, 3072, 12288, 4), (1024, 3072, 3072, 2),
+                       (300, 700, 1024, 3), (512, 3072, 12288, 6)]:
+        _, _, a6, w6, xs, ws, b = operands(native, M, N, K, M + K)
+        out = native.int4_convrot_gemm_bf6(a6, w6, xs, ws, b, native.EPI_F32, nsplit=s)
+        key = (M, N, K, s)
+        if key in first:
+            assert torch.equal(out, first[key]), key
+        first[key] = out
+        wsb = native._workspaces[(torch.cuda.current_device(), st)]
+        assert int(wsb[:native.SPLIT_COUNTER_BYTES].count_nonzero()) == 0, key

@@ -40,7 +40,7 @@ def noalloc(lib, x, w6, ws, b, D, U, R, out, M, N, K):
 
 def workspace_call(lib, x, w6, ws, b, D, U, R, out, M, N, K):
     nbytes = lib.cr_convrot_w4a4_linear_bf6_workspace(M, N, K, R)
-    work = torch.empty((nbytes,), dtype=torch.uint8, device="cuda")
+    work = torch.zeros((nbytes,), dtype=torch.uint8, device="cuda")     # the split counters start at zero
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     return lib.cr_convrot_w4a4_linear_bf6(ptr(x), 1, ptr(w6), ptr(ws), ptr(b), 2, ptr(D), ptr(U), R,
                                           ctypes.c_float(1.0), ptr(out), 1, M, N, K, 256, ptr(work), nbytes, stream)
