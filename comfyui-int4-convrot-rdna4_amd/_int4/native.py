@@ -30,7 +30,7 @@ _IN_DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 EPI_F32, EPI_BF16, EPI_BF16_EAGER, EPI_ACC = 0, 1, 2, 3
 
 # cr_abi_version() of the library these signatures describe
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _vp, _i = ctypes.c_void_p, ctypes.c_int
 _SIGNATURES = {

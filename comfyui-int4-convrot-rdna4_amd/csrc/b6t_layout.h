@@ -59,15 +59,17 @@ __host__ __device__ __forceinline__ int i8t_off(int r, int c) { return r * 64 + 
 // odd 32-row tiles keep dwords d0..d1 in the Q piece (its bytes 8..15)
 __host__ __device__ __forceinline__ bool b6_odd_tile(int r) { return ((r >> 5) & 1) != 0; }
 
-// BF6 code of an integer -8..7: 0 -> 0, |q| = 2^e (1 + m/4) -> (e + 3) << 2 | m, sign 0x20.
-constexpr uint32_t bf6_code_of_int(int q) {
-    if (q == 0) return 0;
-    const int a = q < 0 ? -q : q;
-    int e = 0;
-    while ((a >> (e + 1)) != 0) ++e;
-    const int m = ((a << 2) >> e) & 3;
-    return (q < 0 ? 0x20u : 0u) | (uint32_t)((e + 3) << 2) | (uint32_t)m;
-}
-static_assert(bf6_code_of_int(7) == 23 && bf6_code_of_int(-8) == 56 && bf6_code_of_int(3) == 18, "bf6");
+// BF6 code of an int4 value q (-8..7).  The code holds q / 16: E3M2 (bias 3)
+// spaces its subnormals (m / 16, m = 0..3) and its first binade ((4 + m) / 16)
+// 1/16 apart, and 8 / 16 = 1.0 * 2^-1 is code 0b01000, so the code of q / 16 is
+// |q| itself with the sign in bit 5 (-0, 0x20, is a zero as well).  The GEMMs
+// scale both operands by 2^4 (E8M0 block scale 131), so every product is q_a q_b.
+// On this grid the gfx950 converter (v_cvt_scalef32_pk32_bf6_bf16 with scale
+// 16, which divides) rounds a bf16 value z with |z| <= 8.5 to the code of
+// rint_even(z), signed zeros included: checked on every such bf16 value.
+constexpr uint32_t bf6_code_of_int(int q) { return (q < 0 ? 0x20u : 0u) | (uint32_t)(q < 0 ? -q : q); }
+static_assert(bf6_code_of_int(7) == 7 && bf6_code_of_int(-8) == 0x28 && bf6_code_of_int(-1) == 0x21 &&
+              bf6_code_of_int(0) == 0, "bf6");
+constexpr int B6_OPERAND_E8M0 = 131;   // MFMA block scale of B6T operands: 2^4
 
 }  // namespace convrot

@@ -384,4 +384,4 @@ API int cr_convrot_w4a4_linear_bf6_noalloc(const void* x, int in_dtype, const vo
 
 API int cr_max_quant_k(void) { return convrot::rotquant_max_k(); }
 
-API int cr_abi_version(void) { return 11; }
+API int cr_abi_version(void) { return 12; }

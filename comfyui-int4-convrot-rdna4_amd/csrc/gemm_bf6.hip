@@ -7,8 +7,8 @@
 // product is an integer of magnitude <= 64 K < 2^24 for K < 262144, so the fp32
 // accumulation is exact in any order: the accumulators equal the int32 ones of
 // the reference int4 GEMM bit for bit, and the epilogues are the int8 kernels'
-// (gemm_common.h).  With unit block scales (E8M0 127) the scale operands are
-// exact multiplications by 1.
+// (gemm_common.h).  The B6T codes hold q / 16 (b6t_layout.h); block scales of
+// 2^4 on both operands (E8M0 131) are exact and make every product q_a q_b.
 //
 // Operands are in the B6T layout (b6t_layout.h), produced by
 // int4_to_bf6t_kernel from the packed int4 layout or directly by the fused
@@ -88,11 +88,10 @@ __global__ __launch_bounds__(256) void int4_to_bf6t_kernel(const uint8_t* __rest
     }
 }
 
-// integer value of a BF6 code that holds an int4 value (0 and -0 -> 0,
-// |v| = (4 + m) 2^(e - 5) for exponent field e >= 3, sign bit 0x20)
+// int4 value of a B6T code (bf6_code_of_int: |q| in bits 0..4, sign in bit 5;
+// 0 and -0 -> 0)
 __device__ __forceinline__ int int_of_bf6(uint32_t c) {
-    const int e = (int)((c >> 2) & 7), m = (int)(c & 3);
-    const int a = e < 3 ? 0 : ((4 + m) << e) >> 5;
+    const int a = (int)(c & 31u);
     return (c & 0x20u) ? -a : a;
 }
 
@@ -144,7 +143,6 @@ static_assert(B6_LOADS == 6, "the main loop issues a block's copies in slots 2, 
 constexpr int B6_RING_BYTES = B6_STAGES * B6_STAGE_BYTES;  // 144 KB
 constexpr int B6_LDS_BYTES = B6_RING_BYTES + EPI_SCALE_FLOATS * 4;
 constexpr int BF6_FMT = 3;                                 // f8f6f4 operand format code of BF6 (E3M2)
-constexpr int E8M0_ONE = 127;                              // block scale 2^0
 
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
@@ -251,7 +249,7 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
         const v8i fa = (i & 1) ? bf6_operand_odd(q, p) : bf6_operand_even(p, q);
         const v8i fb = j ? bf6_operand_odd(qb, pb) : bf6_operand_even(pb, qb);
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(   // transposed tile
-                fb, fa, acc[i][j], BF6_FMT, BF6_FMT, 0, E8M0_ONE, 0, E8M0_ONE);
+                fb, fa, acc[i][j], BF6_FMT, BF6_FMT, 0, B6_OPERAND_E8M0, 0, B6_OPERAND_E8M0);
     };
     // the reads issued after MFMA slot t, in the order the next k step's MFMAs
     // consume them: pb0 qb | pa0 qa0 | pb1 pa1 | pa2 qa1 | pa3 (all in the first
@@ -528,7 +526,7 @@ __global__ __launch_bounds__(B6S_THREADS) void w4a4_gemm_bf6_small_kernel(
         const v8i fa = i ? bf6_operand_odd(f.qa, f.pa[1]) : bf6_operand_even(f.pa[0], f.qa);
         const v8i fb = j ? bf6_operand_odd(f.qb, f.pb[1]) : bf6_operand_even(f.pb[0], f.qb);
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(   // transposed tile
-                fb, fa, acc[i][j], BF6_FMT, BF6_FMT, 0, E8M0_ONE, 0, E8M0_ONE);
+                fb, fa, acc[i][j], BF6_FMT, BF6_FMT, 0, B6_OPERAND_E8M0, 0, B6_OPERAND_E8M0);
     };
     // reads issued after MFMA slot t, in the order the next k step consumes them:
     // pa0 qa | pb0 qb | pb1 pa1

@@ -636,12 +636,20 @@ __global__ __launch_bounds__(64 * MAXW) __attribute__((amdgpu_waves_per_eu(4, 5)
 #pragma unroll
             for (int i = 0; i < 16; i += 2) {
                 float z0, z1;
+                const int e0 = final_elem<G>(gl, i), e1 = final_elem<G>(gl, i + 1);
                 if constexpr (DT == DT_BF16) {
                     // one packed RNE for both quotients; |z| <= QMAX (1 + 2^-9) because
                     // s = RNE(absmax / QMAX), so rint stays in [-QMAX, QMAX]; the int8
                     // clamp only guards non-finite input
                     const uint32_t zz = pack_bf16x2(bf16lo_to_f32(hv[p].w[i >> 1]) * rinv32,
                                                     bf16hi_to_f32(hv[p].w[i >> 1]) * rinv32);
+                    if constexpr (B6) {
+                        // the bf16 quotients as they are: the BF6 conversion (scale 16)
+                        // rounds each to the code of rint_even(z), |z| <= 7 (1 + 2^-9)
+                        *b6_slot(gfirst + e0 / kChunk, e0 % kChunk, p & 1) = (uint16_t)zz;
+                        *b6_slot(gfirst + e1 / kChunk, e1 % kChunk, p & 1) = (uint16_t)(zz >> 16);
+                        continue;
+                    }
                     z0 = bf16lo_to_f32(zz);
                     z1 = bf16hi_to_f32(zz);
                     if constexpr (INT8) {
@@ -662,10 +670,11 @@ __global__ __launch_bounds__(64 * MAXW) __attribute__((amdgpu_waves_per_eu(4, 5)
                     z0 = zz[0];
                     z1 = zz[1];
                 }
-                const int e0 = final_elem<G>(gl, i), e1 = final_elem<G>(gl, i + 1);
                 if constexpr (B6) {
-                    // rint_even(z) as a float, kept as its bf16 bits (exact: an integer of
-                    // magnitude <= 7; a zero code may carry the sign of z)
+                    // f16 / f32 input: the DT-rounded quotient would not survive a bf16
+                    // rounding, so rint_even(z) here, kept as its bf16 bits (exact: an
+                    // integer of magnitude <= 7; a zero code may carry the sign of z),
+                    // which the conversion maps to its code unchanged
                     const float q0 = __builtin_rintf(z0), q1 = __builtin_rintf(z1);
                     *b6_slot(gfirst + e0 / kChunk, e0 % kChunk, p & 1) = (uint16_t)(__float_as_uint(q0) >> 16);
                     *b6_slot(gfirst + e1 / kChunk, e1 % kChunk, p & 1) = (uint16_t)(__float_as_uint(q1) >> 16);
@@ -696,7 +705,9 @@ __global__ __launch_bounds__(64 * MAXW) __attribute__((amdgpu_waves_per_eu(4, 5)
                     if (live) {
                         const v16u words = {gq[0].x, gq[0].y, gq[0].z, gq[0].w, gq[1].x, gq[1].y, gq[1].z, gq[1].w,
                                             gq[2].x, gq[2].y, gq[2].z, gq[2].w, gq[3].x, gq[3].y, gq[3].z, gq[3].w};
-                        const v6u r = __builtin_amdgcn_cvt_scalef32_pk32_bf6_bf16(__builtin_bit_cast(v32bf, words), 1.0f);
+                        // scale 16: the code of round(value / 16) on E3M2's 1/16 grid = the
+                        // B6T code of rint_even(value) (b6t_layout.h)
+                        const v6u r = __builtin_amdgcn_cvt_scalef32_pk32_bf6_bf16(__builtin_bit_cast(v32bf, words), 16.0f);
 #pragma unroll
                         for (int i = 0; i < 6; ++i) fd[p >> 1][i] = r[i];
                     }

@@ -156,9 +156,12 @@ int cr_int4_convrot_gemm_lora(const void* Xp, const void* Wp, const void* xscale
  *
  * "B6T" layout of a [rows, K] operand (K % 128 == 0): rows padded to
  * R = ceil(rows / 256) * 256 with zero codes; R * 3K/4 bytes stored as
- * [R / 256][K / 128] chunks of 24576 bytes (256 rows x 128 k).  Group g of a
- * row is the 32 BF6 codes of k = 128 kb + 32 g .. +31, code e at bits
- * 6e..6e+5 of the group's 6 little-endian dwords d0..d5.  In a chunk, with
+ * [R / 256][K / 128] chunks of 24576 bytes (256 rows x 128 k).  An int4
+ * value q is held as the BF6 code of q / 16, which is |q| with the sign in bit
+ * 5 (E3M2's subnormals and first binade are 1/16 apart; -0, 0x20, may stand
+ * for 0); the GEMMs scale both operands by 2^4.  Group g of a row is the 32
+ * codes of k = 128 kb + 32 g .. +31, code e at bits 6e..6e+5 of the group's
+ * 6 little-endian dwords d0..d5.  In a chunk, with
  * rr = r % 32 and f(rr) = ((rr >> 1 ^ rr >> 3) & 1) | (rr >> 1 & 2):
  *   bytes 0..16383: row r at r * 64; 16-byte piece g ^ f(rr) holds d0..d3 of
  *     group g when r / 32 is even, d2..d5 when it is odd;

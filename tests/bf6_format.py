@@ -1,8 +1,9 @@
 """numpy helpers for the operand layouts of the GEMM paths (test helper): the B6T decoder of the bf6 path and the I8T re-layout of the W8A8 path.
 
 B6T of a [rows, K] matrix (K % 128 == 0): rows padded to R = ceil(rows/256)*256
-(zero codes), stored as [R/256][K/128] chunks of 24576 bytes.  Group g of row r
-= the 32 BF6 (E3M2, bias 3) codes of k = 128 kb + 32 g .. +31, code e at bits
+(zero codes), stored as [R/256][K/128] chunks of 24576 bytes.  An int4 value q
+is held as the BF6 (E3M2, bias 3) code of q / 16 (the GEMM scales both operands
+by 2^4).  Group g of row r = the 32 codes of k = 128 kb + 32 g .. +31, code e at bits
 6e .. 6e+5 of 6 little-endian dwords d0..d5.  In a chunk, with T = r // 32,
 rr = r % 32 and f(rr) = ((rr>>1 ^ rr>>3) & 1) | (rr>>1 & 2): the 16-byte piece
 g ^ f(rr) at r*64 holds d0..d3 (T even) or d2..d5 (T odd); the 16-byte piece
@@ -51,8 +52,8 @@ def decode_b6t(b6: np.ndarray, rows: int) -> np.ndarray:
     grp = np.where(odd[None, None, :, None, None], odd_bytes, even_bytes)   # [T, nkb, 256, 4, 24]
     bits = np.unpackbits(grp, axis=-1, bitorder="little")
     code = (bits.reshape(*grp.shape[:-1], 32, 6) * (1 << np.arange(6))).sum(-1)   # [T, nkb, 256, 4, 32]
-    vals = bf6_value(code)
-    assert np.all(vals == np.round(vals)), "non-integer bf6 code"
+    vals = bf6_value(code) * 16.0                                       # codes hold q / 16
+    assert np.all(vals == np.round(vals)), "bf6 code off the 1/16 grid"
     full = vals.transpose(0, 2, 1, 3, 4).reshape(R, K).astype(np.int64)
     assert not full[rows:].any(), "padding rows must hold zero codes"
     return full[:rows]

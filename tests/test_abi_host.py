@@ -92,7 +92,7 @@ def test_load_refuses_other_abi_version(native, monkeypatch):
 
 def test_library_queries_without_gpu(native):
     lib = native.load_library()
-    assert lib.cr_abi_version() == native.ABI_VERSION == 11
+    assert lib.cr_abi_version() == native.ABI_VERSION == 12
     assert lib.cr_max_quant_k() == 32768
     assert lib.cr_max_quant_bf6_k() == 32768
 

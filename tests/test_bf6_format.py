@@ -1,18 +1,18 @@
 """CPU check of the B6T layout decoder used by the bf6 GPU tests: an
-independent bit-by-bit encoder (integers -> E3M2 codes -> packed groups ->
+independent bit-by-bit encoder (integers q -> E3M2 codes of q / 16 -> packed groups ->
 swizzled, tile-major chunks) must decode back to the integers."""
 import numpy as np
 
 from bf6_format import CHUNK, QOFF, bf6_value, decode_b6t, unpack_int4
 
 
+_VALUES = bf6_value(np.arange(64))
+
+
 def enc(q: int) -> int:
-    if q == 0:
-        return 0
-    a = abs(q)
-    e = a.bit_length() - 1
-    m = ((a << 2) >> e) & 3
-    return (0x20 if q < 0 else 0) | ((e + 3) << 2) | m
+    """The E3M2 code whose value is q / 16, found by search over all 64 codes
+    (+0 for 0)."""
+    return int(np.nonzero(_VALUES == q / 16.0)[0].min())
 
 
 def f(r: int) -> int:
@@ -47,9 +47,13 @@ def encode_b6t(q: np.ndarray) -> np.ndarray:
 
 
 def test_e3m2_codes_of_int4_values():
+    """E3M2's subnormals and first binade are 1/16 apart, so the code of q / 16 is
+    |q| with the sign in bit 5 (what the kernels' bf6_code_of_int writes)."""
     vals = np.arange(-8, 8)
-    assert np.array_equal(bf6_value(np.array([enc(int(q)) for q in vals])), vals)
-    assert [enc(q) for q in (1, 2, 3, 7, -8)] == [12, 16, 18, 23, 56]
+    assert np.array_equal(bf6_value(np.array([enc(int(q)) for q in vals])) * 16, vals)
+    assert [enc(q) for q in (1, 2, 3, 4, 7, -1, -8)] == [1, 2, 3, 4, 7, 0x21, 0x28]
+    assert all(enc(int(q)) == ((0x20 if q < 0 else 0) | abs(int(q))) for q in vals)
+    assert bf6_value(np.array([0x20]))[0] == 0.0                     # -0 is a zero code
 
 
 def test_decoder_inverts_reference_encoder():
