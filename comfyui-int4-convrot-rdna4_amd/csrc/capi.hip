@@ -43,10 +43,7 @@ hipError_t gemm_splitk_launch(const int8_t* Xp, const int8_t* Wp, const float* x
 
 #define API extern "C" __attribute__((visibility("default")))
 
-// Bytes 0 .. 2047 of every workspace this library takes hold the split
-// counters of the bf6 GEMM: zero when a workspace is first used, and zero
-// again after every call (nothing else is ever written there).
-constexpr size_t kSplitCounterBytes = 2048;
+using convrot::kSplitCounterBytes;   // the workspaces' leading counter region (common.h)
 
 static int quant_args_ok(int in_dtype, int M, int K, int G) {
     if (!(G == 16 || G == 64 || G == 256)) return 0;

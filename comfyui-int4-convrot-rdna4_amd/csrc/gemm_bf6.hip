@@ -668,9 +668,8 @@ __global__ __launch_bounds__(64 * B6R_WAVES) void w4a4_bf6_splitk_reduce_kernel(
 bool gemm_bf6_small_tiles(int M, int N, int K);
 
 // Every split workspace starts with the counters of the quarter-tile kernel's
-// split (B6S_MAX_SPLIT_TILES of them); the partials follow.
-constexpr int BF6_SPLIT_COUNTER_BYTES = B6S_MAX_SPLIT_TILES * 4;
-static_assert(BF6_SPLIT_COUNTER_BYTES == 2048, "counter region of the documented workspace layout");
+// split (B6S_MAX_SPLIT_TILES of them, kSplitCounterBytes); the partials follow.
+static_assert(B6S_MAX_SPLIT_TILES * 4 == kSplitCounterBytes, "counter region of the documented workspace layout");
 
 template <int EPI, int LR>
 static hipError_t launch_bf6(const uint8_t* A6, const uint8_t* W6, const float* xs, const float* ws,
@@ -685,7 +684,7 @@ static hipError_t launch_bf6(const uint8_t* A6, const uint8_t* W6, const float* 
     unsigned* cnt = nullptr;
     if (nsplit > 1) {
         cnt = reinterpret_cast<unsigned*>(part);
-        part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(part) + BF6_SPLIT_COUNTER_BYTES);
+        part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(part) + kSplitCounterBytes);
     }
     if (gemm_bf6_small_tiles(M, N, K)) {
         const int sm = (M + B6S_BM - 1) / B6S_BM;
@@ -853,7 +852,7 @@ size_t gemm_bf6_splitk_workspace(int M, int N, int nsplit) {
     const size_t qtiles = (size_t)((M + B6S_BM - 1) / B6S_BM) * ((N + B6S_BN - 1) / B6S_BN);
     const size_t full = (size_t)nsplit * tiles * 8 * 8192 * sizeof(float);
     const size_t small = (size_t)nsplit * qtiles * B6S_PART_FLOATS * sizeof(float);
-    return nsplit <= 1 ? 0 : BF6_SPLIT_COUNTER_BYTES + (full > small ? full : small);
+    return nsplit <= 1 ? 0 : kSplitCounterBytes + (full > small ? full : small);
 }
 
 }  // namespace convrot
