@@ -583,7 +583,9 @@ def bench_gemm_sweep(args):
             timer.close()
             med = us[len(us) // 2]
             ops = 2.0 * M * N * K
-            detail[f"{M}x{K}->{N}"] = {"us": round(med, 2), "TOPS": round(ops / med / 1e6, 1), "nsplit": ns}
+            bm, bn = native.gemm_tile_bf6(M, N, K, ns)
+            detail[f"{M}x{K}->{N}"] = {"us": round(med, 2), "TOPS": round(ops / med / 1e6, 1), "nsplit": ns,
+                                       "tile": f"{bm}x{bn}"}
             total_ops += ops
             total_s += med * 1e-6
             del a6, out, wsp

@@ -30,7 +30,7 @@ _IN_DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 EPI_F32, EPI_BF16, EPI_BF16_EAGER, EPI_ACC = 0, 1, 2, 3
 
 # cr_abi_version() of the library these signatures describe
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _vp, _i = ctypes.c_void_p, ctypes.c_int
 _SIGNATURES = {
@@ -57,6 +57,7 @@ _SIGNATURES = {
     "cr_int8_convrot_gemm_i8t": ([_vp] * 6 + [_i] * 4 + [_vp], _i),
     "cr_gemm_bf6_choose_nsplit": ([_i, _i, _i], _i),
     "cr_gemm_bf6_splitk_workspace": ([_i, _i, _i], ctypes.c_size_t),
+    "cr_gemm_bf6_tile": ([_i, _i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)], _i),
     "cr_int4_convrot_gemm_bf6_splitk": ([_vp] * 7 + [_i, ctypes.c_float, _vp] + [_i] * 5 + [_vp, ctypes.c_size_t, _vp],
                                         _i),
     "cr_convrot_w4a4_linear_bf6": ([_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _i, ctypes.c_float, _vp] + [_i] * 5
@@ -467,6 +468,14 @@ def _bf6_gemm_args(a6, w6, x_scale, w_scale, bias, M, N):
 def choose_nsplit_bf6(M: int, N: int, K: int) -> int:
     """The library's k-split count for an M x N x K bf6 GEMM (1: no split)."""
     return int(load_library().cr_gemm_bf6_choose_nsplit(M, N, K))
+
+
+def gemm_tile_bf6(M: int, N: int, K: int, nsplit: int = 1) -> tuple[int, int]:
+    """The workgroup tile (rows of A, rows of B) of a bf6 GEMM launch."""
+    bm, bn = ctypes.c_int(0), ctypes.c_int(0)
+    if load_library().cr_gemm_bf6_tile(M, N, K, nsplit, ctypes.byref(bm), ctypes.byref(bn)) != 0:
+        raise ValueError(f"no bf6 GEMM launch takes M={M} N={N} K={K} nsplit={nsplit}")
+    return bm.value, bn.value
 
 
 def _bf6_launch(a6, w6, xs, wsc, b, t, up, R, scale, out, M, N, K, epilogue, nsplit):

@@ -37,6 +37,7 @@ hipError_t int8_to_i8t_launch(const void* src, void* dst, int rows, int K, hipSt
 hipError_t gemm_i8t_launch(const int8_t* X, const int8_t* W, const float* xs, const float* ws,
                            const float* bias, void* out, int M, int N, int K, int epi, hipStream_t st);
 size_t gemm_bf6_splitk_workspace(int M, int N, int nsplit);
+void gemm_bf6_tile(int M, int N, int K, int nsplit, int* bm, int* bn);
 hipError_t gemm_splitk_launch(const int8_t* Xp, const int8_t* Wp, const float* xs, const float* ws, float* accum,
                               int M, int N, int K, int nsplit, hipStream_t st);
 }  // namespace convrot
@@ -178,6 +179,13 @@ API int cr_int4_convrot_gemm_bf6_lora(const void* A6, const void* W6, const void
 API int cr_gemm_bf6_choose_nsplit(int M, int N, int K) {
     if (M <= 0 || N <= 0 || !bf6_k_ok(K)) return 1;
     return convrot::gemm_bf6_choose_nsplit(M, N, K);
+}
+
+API int cr_gemm_bf6_tile(int M, int N, int K, int nsplit, int* bm, int* bn) {
+    if (M <= 0 || N <= 0 || !bf6_k_ok(K) || nsplit < 1 || nsplit > K / 128 || bm == nullptr || bn == nullptr)
+        return -1;
+    convrot::gemm_bf6_tile(M, N, K, nsplit, bm, bn);
+    return 0;
 }
 
 API size_t cr_gemm_bf6_splitk_workspace(int M, int N, int nsplit) {
@@ -389,4 +397,4 @@ API int cr_convrot_w4a4_linear_bf6_noalloc(const void* x, int in_dtype, const vo
 
 API int cr_max_quant_k(void) { return convrot::rotquant_max_k(); }
 
-API int cr_abi_version(void) { return 12; }
+API int cr_abi_version(void) { return 13; }

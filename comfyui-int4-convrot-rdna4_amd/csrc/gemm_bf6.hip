@@ -401,60 +401,85 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Small grids: a 128 x 128 tile per 256-lane workgroup of 4 waves (2 x 2 of
-// 64 x 64 = 2 x 2 MFMA 32 x 32 tiles, 8 MFMAs per 128-k block and wave).  With
-// 256 x 256 tiles a grid of few row tiles (M <= 1024 or so) leaves most CUs
-// idle; a quarter tile quadruples the workgroups at 1.5x the operand bytes
-// per MAC.  A stage is the tile's halves of the A and B chunks of one 128-k
-// block: rows h*128 .. h*128+127 of a B6T chunk are its P bytes h*8192 ..
-// +8191 and its Q row pairs 2h, 2h+1 (bytes 16384 + h*4096 .. +4095), copied
-// into LDS as [P 8 KB][Q 4 KB] (12 KB per operand, 24 KB per stage, 6 DMA
-// instructions per wave), three stages: 75 KB of LDS, two workgroups per CU.
-// The fragment offsets of a local row rl are those of the full chunk with
-// the Q part at 8192 (the swizzle depends on row bits 1..4 only).  Same
-// two-phase schedule as the big kernel: per phase 4 MFMAs, each of the first
-// three followed by the next k step's fragment reads in consumption order and
-// by one DMA instruction (phase A: the second half of block kb+2, phase B: the
-// first half of block kb+3).  Same accumulators, same epilogue: the outputs
-// equal the 256 x 256 kernel's bit for bit.
+// Small grids: tiles of UA x UB units of 64 rows (BM = 64 UA rows of A, BN =
+// 64 UB rows of B), one wave per 64 x 64 piece (2 x 2 MFMA 32 x 32 tiles, 8
+// MFMAs per 128-k block and wave).  With 256 x 256 tiles a grid of few row
+// tiles (M <= 2048 or so) leaves most CUs idle.  Two shapes are built: 128 x
+// 128 (the quarter tile, 4 waves, three stages) and 128 x 192 (6 waves, four
+// stages), the latter for grids whose 128 x 128 tiles would put two
+// workgroups on some CUs while its own cover the CUs once
+// (gemm_bf6_small_shape below).
+// A 64-row unit of a B6T chunk (rows 64h .. 64h+63) is its P bytes h*4096 ..
+// +4095 and its Q rows 32h .. 32h+31 (bytes 16384 + h*2048 .. +2047), copied
+// into LDS as [P 4 KB][Q 2 KB]: a stage is the tile's A units, then its B
+// units, of one 128-k block (6 KB, 6 DMA instructions per unit), in a ring
+// of NST stages.  A wave's 64 rows of A are one unit, and so are its 64 rows of
+// B: the fragment offsets of a local row rl < 64 are those of the full chunk
+// with the unit's Q part at 4096 (the swizzle depends on row bits 1..4 only).
+// Units of an edge tile past the operand's padded rows re-read the last unit
+// (they feed only outputs that are never stored).  Same two-phase schedule as
+// the big kernel: per phase 4 MFMAs, the first three each followed by the
+// next k step's fragment reads in consumption order and by a third of the
+// phase's DMA instructions (phase A: the second part of block kb+NST-1,
+// phase B: the first part of block kb+NST).  Same accumulators, same epilogue: the
+// outputs equal the 256 x 256 kernel's bit for bit.
 //
-// SPLIT (S = nsplit > 1): workgroup b takes tile b % T and the 128-k blocks
-// [s nkb / S, (s + 1) nkb / S) of split s = b / T.  Every workgroup stores its
-// raw accumulators (exact integers in fp32) in the workspace with device-scope
-// stores, waits until they are done and takes a ticket from the tile's
-// counter; the one that draws the last ticket adds the other S - 1 partials to
-// its own (exact in any order: integers below 2^24), sets the counter back to
-// zero and runs the epilogue.
+// SPLIT (S = nsplit > 1, the 128 x 128 shape only): workgroup b takes tile
+// b % T and the 128-k blocks [s nkb / S, (s + 1) nkb / S) of split s = b / T.
+// Every workgroup stores its raw accumulators (exact integers in fp32) in the
+// workspace with device-scope stores, waits until they are done and takes a
+// ticket from the tile's counter; the one that draws the last ticket adds the
+// other S - 1 partials to its own (exact in any order: integers below 2^24),
+// sets the counter back to zero and runs the epilogue.
 // No workgroup waits for another, so no launch order or residency can stall
 // the grid.  The counters (one per tile, at most 512) must be zero when a
 // workspace is first used; every call leaves them zero.
 // ---------------------------------------------------------------------------
-constexpr int B6S_BM = 128, B6S_BN = 128;
-constexpr int B6S_THREADS = 256;
-constexpr int B6S_STAGES = 3;                                  // 4 and 6 measured no faster
-constexpr int B6S_HALF = B6_CHUNK / 2;                         // 12 KB: one operand half chunk
-constexpr int B6S_STAGE_BYTES = 2 * B6S_HALF;                  // 24 KB
-constexpr int B6S_LOADS = B6S_STAGE_BYTES / 16 / B6S_THREADS;  // 6 DMA instructions per lane
-static_assert(B6S_LOADS == 6, "three copies per phase");
-static_assert((B6S_STAGES - 2) * B6S_LOADS + B6S_LOADS / 2 <= 63, "vmcnt range");
-constexpr int B6S_RING_BYTES = B6S_STAGES * B6S_STAGE_BYTES;
-constexpr int B6S_LDS_BYTES = B6S_RING_BYTES + EPI_SCALE_FLOATS * 4 + 16;   // + the split ticket
+constexpr int B6S_UNIT = 6144;                                  // 64 rows of a chunk: P 4 KB + Q 2 KB
+constexpr int B6S_UNIT_Q = 4096;                                // Q part inside a unit
+constexpr int B6S_STAGES = 3;                                   // 128 x 128: 4 and 6 measured no faster
 constexpr int B6S_MAX_SPLIT_TILES = 512;                        // split counters per workspace
-constexpr int B6S_PART_FLOATS = B6S_BM * B6S_BN;                // one tile's partial: 64 KB
+constexpr int B6S_BM = 128, B6S_BN = 128;                       // the split shape
+constexpr int B6S_PART_FLOATS = B6S_BM * B6S_BN;                // one split tile's partial: 64 KB
 
-template <int EPI, int LR, bool SPLIT>
-__global__ __launch_bounds__(B6S_THREADS) void w4a4_gemm_bf6_small_kernel(
+template <int UA, int UB, int NST_ = B6S_STAGES>
+struct B6Small {
+    static constexpr int NST = NST_;                            // ring stages
+    static constexpr int BM = 64 * UA, BN = 64 * UB;
+    static constexpr int WAVES = UA * UB;
+    static constexpr int THREADS = 64 * WAVES;
+    static constexpr int UNITS = UA + UB;
+    static constexpr int STAGE_BYTES = UNITS * B6S_UNIT;
+    static constexpr int LOADS = 6 * UNITS / WAVES;             // DMA instructions per wave and block
+    static constexpr int LOADS_B = LOADS / 2;                    // first part: NST blocks ahead, phase B
+    static constexpr int LOADS_A = LOADS - LOADS_B;              // second part: NST-1 blocks ahead, phase A
+    static constexpr int RING_BYTES = NST * STAGE_BYTES;
+    static constexpr int LDS_BYTES = RING_BYTES + EPI_SCALE_FLOATS * 4 + 16;   // + the split ticket
+    static_assert(6 * UNITS % WAVES == 0, "whole DMA instructions per wave");
+    static_assert((NST - 2) * LOADS + LOADS_B <= 63 && NST >= 3, "vmcnt range");
+    static_assert(BM <= 256 && BN <= 256 && THREADS >= BM && THREADS >= BN, "staged scales");
+};
+static_assert(B6Small<2, 2>::BM == B6S_BM && B6Small<2, 2>::BN == B6S_BN, "split shape");
+
+// tile shapes of the small kernel (gemm_bf6_small_shape)
+enum : int { SMALL_128x128 = 0, SMALL_128x192 = 1 };
+constexpr int B6S_STAGES_192 = 4;                              // ring stages of the 128 x 192 shape
+
+template <int EPI, int LR, bool SPLIT, int UA, int UB, int NSTAGES>
+__global__ __launch_bounds__(64 * UA * UB) void w4a4_gemm_bf6_small_kernel(
         const uint8_t* __restrict__ A6, const uint8_t* __restrict__ W6,
         const float* __restrict__ xs, const float* __restrict__ ws, const void* __restrict__ bias, int bias_dt,
         void* __restrict__ out, int M, int N, int K, LoraArgs lora, int gm, int nsplit,
         float* __restrict__ part, unsigned* __restrict__ cnt) {
+    using S = B6Small<UA, UB, NSTAGES>;
+    static_assert(!SPLIT || (UA == 2 && UB == 2), "the split runs on the 128 x 128 shape");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds6[];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int tiles_m = (M + B6S_BM - 1) / B6S_BM, tiles_n = (N + B6S_BN - 1) / B6S_BN;
+    const int wm = wave / UB, wn = wave % UB;
+    const int tiles_m = (M + S::BM - 1) / S::BM, tiles_n = (N + S::BN - 1) / S::BN;
     const int nkb_all = K / 128;
     int tm, tn, kb0 = 0, nkb = nkb_all, split = 0, tix = blockIdx.x;
     if constexpr (SPLIT) {
@@ -465,29 +490,39 @@ __global__ __launch_bounds__(B6S_THREADS) void w4a4_gemm_bf6_small_kernel(
         nkb = (int)((long long)(split + 1) * nkb_all / nsplit) - kb0;
     }
     tile_of_block(tix, tiles_m, tiles_n, gm, tm, tn);
-    const int m0 = tm * B6S_BM;
-    const int n0 = tn * B6S_BN;
+    const int m0 = tm * S::BM;
+    const int n0 = tn * S::BN;
 
-    float* sc = reinterpret_cast<float*>(lds6 + B6S_RING_BYTES);
+    float* sc = reinterpret_cast<float*>(lds6 + S::RING_BYTES);
     ScaleRegs scr;                                              // staged in LDS after the main loop
     scr.load(xs, ws, bias, bias_dt, M, N, m0, n0, tid);
 
-    // copy j (0..5) of this wave is instruction w*6 + j of the stage's 24: 0..11
-    // the A half (8 P KB, then 4 Q KB), 12..23 the B half
+    // Copy j (0 .. LOADS-1) of this wave is instruction i = wave * LOADS + j of the
+    // stage's 6 UNITS: KB i % 6 (P 0..3, Q 4..5) of unit i / 6 (A units, then B
+    // units).  Per copy: its source at the split's first block, and its LDS offset
+    // inside a stage (wave-uniform).
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    const uint8_t* a_chunks = A6 + ((size_t)(m0 >> 8) * nkb_all + kb0) * B6_CHUNK;
-    const uint8_t* b_chunks = W6 + ((size_t)(n0 >> 8) * nkb_all + kb0) * B6_CHUNK;
-    const int a_half = (m0 >> 7) & 1, b_half = (n0 >> 7) & 1;
+    const int last_a = ((M + 255) >> 8) * 4 - 1, last_b = ((N + 255) >> 8) * 4 - 1;   // last 64-row units
+    const uint8_t* csrc[S::LOADS];
+    uint32_t cdst[S::LOADS];
+#pragma unroll
+    for (int j = 0; j < S::LOADS; ++j) {
+        const int ins = wave_u * S::LOADS + j;
+        const int u = ins / 6, o = ins - 6 * u;
+        const bool is_a = u < UA;
+        const int gr = is_a ? min((m0 >> 6) + u, last_a) : min((n0 >> 6) + u - UA, last_b);   // 64-row unit
+        const int h = gr & 3;
+        const int off = o < 4 ? h * 4096 + o * 1024 : B6_QOFF + h * 2048 + (o - 4) * 1024;
+        csrc[j] = (is_a ? A6 : W6) + ((size_t)(gr >> 2) * nkb_all + kb0) * B6_CHUNK + off + lane * 16;
+        cdst[j] = (uint32_t)(uintptr_t)lds6 + u * B6S_UNIT + o * 1024;
+    }
     auto dma_one = [&](int kb, int j) __attribute__((always_inline)) {
-        const int ins = wave_u * B6S_LOADS + j;                    // wave-uniform, 0..23
-        const bool is_a = ins < 12;
-        const int o = is_a ? ins : ins - 12;                       // KB inside the half image
-        const int h = is_a ? a_half : b_half;
-        const int src_off = o < 8 ? h * 8192 + o * 1024 : B6_QOFF + h * 4096 + (o - 8) * 1024;
-        const uint8_t* chunk = (is_a ? a_chunks : b_chunks) + (size_t)min(kb, nkb - 1) * B6_CHUNK;
-        const uint32_t st = (uint32_t)(uintptr_t)lds6 + (kb % B6S_STAGES) * B6S_STAGE_BYTES +
-                            (is_a ? 0 : B6S_HALF) + o * 1024;
-        dma16(st, chunk + src_off + lane * 16);
+        dma16(cdst[j] + (kb % S::NST) * S::STAGE_BYTES, csrc[j] + (size_t)min(kb, nkb - 1) * B6_CHUNK);
+    };
+    // the copies of one part issued after MFMA slot t (1..3) of a phase: a third each
+    auto dma_part = [&](int kb, int t, int first, int n) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = n * (t - 1) / 3; j < n * t / 3; ++j) dma_one(kb, first + j);
     };
 
     v16f acc[2][2];
@@ -499,18 +534,16 @@ __global__ __launch_bounds__(B6S_THREADS) void w4a4_gemm_bf6_small_kernel(
     const int frow = lane & 31;
     const int fhalf = lane >> 5;
     // per-lane byte offsets (inside a stage) of this lane's P and Q pieces for the
-    // two k steps; the wave's second A / B row tile sits 2048 bytes further in P
+    // two k steps; the wave's A rows are unit wm, its B rows unit UA + wn, and its
+    // second row tile of either sits 2048 bytes further in P
     uint32_t offPa[2], offQa[2], offPb[2], offQb[2];
-    {
-        const int ra = wm * 64 + frow, rb = wn * 64 + frow;
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-            const int g = 2 * s2 + fhalf;
-            offPa[s2] = b6_p_off(ra, g);
-            offQa[s2] = b6_q_off(ra, g) - B6_QOFF + 8192;
-            offPb[s2] = B6S_HALF + b6_p_off(rb, g);
-            offQb[s2] = B6S_HALF + b6_q_off(rb, g) - B6_QOFF + 8192;
-        }
+    for (int s2 = 0; s2 < 2; ++s2) {
+        const int g = 2 * s2 + fhalf;
+        offPa[s2] = wm * B6S_UNIT + b6_p_off(frow, g);
+        offQa[s2] = wm * B6S_UNIT + B6S_UNIT_Q + b6_q_off(frow, g) - B6_QOFF;
+        offPb[s2] = (UA + wn) * B6S_UNIT + b6_p_off(frow, g);
+        offQb[s2] = (UA + wn) * B6S_UNIT + B6S_UNIT_Q + b6_q_off(frow, g) - B6_QOFF;
     }
     struct Frags { v4u pa[2], qa, pb[2], qb; };
     auto read_one = [&](uint32_t st, int s2, int r, Frags& f) __attribute__((always_inline)) {
@@ -537,43 +570,43 @@ __global__ __launch_bounds__(B6S_THREADS) void w4a4_gemm_bf6_small_kernel(
     };
 
     // Ring of NST stages, block b in stage b % NST: blocks 0 .. NST-2 and the
-    // first half of NST-1 in the prologue; at block kb, phase A copies the second
-    // half of block kb+NST-1 (into block kb-1's stage) and phase B the first
-    // half of block kb+NST (into block kb's stage, free after the barrier).
-    constexpr int NST = B6S_STAGES;
+    // first part of NST-1 in the prologue; at block kb, phase A copies the second
+    // part of block kb+NST-1 (into block kb-1's stage) and phase B the first
+    // part of block kb+NST (into block kb's stage, free after the barrier).
+    constexpr int NST = S::NST;
     Frags F0, F1;
 #pragma unroll
     for (int b = 0; b < NST - 1; ++b)
 #pragma unroll
-        for (int j = 0; j < B6S_LOADS; ++j) dma_one(b, j);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * B6S_LOADS));   // block 0 landed, blocks 1 .. NST-2 in flight
+        for (int j = 0; j < S::LOADS; ++j) dma_one(b, j);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * S::LOADS));   // block 0 landed, blocks 1 .. NST-2 in flight
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < B6S_LOADS / 2; ++j) dma_one(NST - 1, j);   // first half; the second in phase A of block 0
+    for (int j = 0; j < S::LOADS_B; ++j) dma_one(NST - 1, j);   // first part; the second in phase A of block 0
 #pragma unroll
     for (int r = 0; r < 6; ++r) read_one(0, 0, r, F0);
     uint32_t st_cur = 0;
     for (int kb = 0; kb < nkb; ++kb) {
-        const uint32_t st_nxt = st_cur == (NST - 1) * B6S_STAGE_BYTES ? 0u : st_cur + B6S_STAGE_BYTES;
+        const uint32_t st_nxt = st_cur == (NST - 1) * S::STAGE_BYTES ? 0u : st_cur + S::STAGE_BYTES;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             mfma_one(F0, t);
             __builtin_amdgcn_sched_barrier(0);
-            if (t >= 1) dma_one(kb + NST - 1, B6S_LOADS / 2 + t - 1);
+            if (t >= 1) dma_part(kb + NST - 1, t, S::LOADS_B, S::LOADS_A);
             reads_after(t, st_cur, 1, F1);
             __builtin_amdgcn_sched_barrier(0);
         }
         // this wave's copies of block kb+1 landed (those of blocks kb+2 .. kb+NST-1
-        // may be in flight) and its reads of block kb done: after the barrier
-        // block kb's stage is free
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * B6S_LOADS) & 0xc07f);
+        // may be in flight) and its reads of block kb done: after the barrier block
+        // kb's stage is free
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((NST - 2) * S::LOADS) & 0xc07f);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             mfma_one(F1, t);
             __builtin_amdgcn_sched_barrier(0);
-            if (t >= 1) dma_one(kb + NST, t - 1);
+            if (t >= 1) dma_part(kb + NST, t, 0, S::LOADS_B);
             reads_after(t, st_nxt, 0, F0);
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -587,7 +620,7 @@ __global__ __launch_bounds__(B6S_THREADS) void w4a4_gemm_bf6_small_kernel(
         // relaxed atomic accesses (coherent across the XCDs' L2 caches without writing an L2 back);
         // each wave's vmcnt(0) before the barrier orders its stores before the ticket.
         const int T = tiles_m * tiles_n;
-        auto slot = [&](int s) { return part + ((size_t)(s * T + tix) * 4 + wave) * 4096 + lane; };
+        auto slot = [&](int s) { return part + ((size_t)(s * T + tix) * S::WAVES + wave) * 4096 + lane; };
         float* dst = slot(split);
 #pragma unroll
         for (int q = 0; q < 64; ++q)
@@ -597,7 +630,7 @@ __global__ __launch_bounds__(B6S_THREADS) void w4a4_gemm_bf6_small_kernel(
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));             // this wave's partial is stored
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __syncthreads();                                      // ... and every other wave's
-        unsigned* ticket = reinterpret_cast<unsigned*>(lds6 + B6S_RING_BYTES + EPI_SCALE_FLOATS * 4);
+        unsigned* ticket = reinterpret_cast<unsigned*>(lds6 + S::RING_BYTES + EPI_SCALE_FLOATS * 4);
         if (tid == 0) *ticket = __hip_atomic_fetch_add(cnt + tix, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         if (*ticket != (unsigned)nsplit - 1) return;          // another split finishes this tile
@@ -616,7 +649,7 @@ __global__ __launch_bounds__(B6S_THREADS) void w4a4_gemm_bf6_small_kernel(
     __syncthreads();
     int em0 = m0, en0 = n0, elane = lane;
     asm volatile("" : "+s"(M), "+s"(N), "+v"(em0), "+v"(en0), "+v"(elane));
-    constexpr int SCR = B6S_RING_BYTES / (B6S_THREADS / 64);
+    constexpr int SCR = S::RING_BYTES / S::WAVES;
     epilogue_lds<EPI, 2, 2, LR, SCR>(acc, sc, out, M, N, em0, en0, em0 + wm * 64, en0 + wn * 64, elane, lora,
                                      lds6 + wave * SCR);
 }
@@ -666,6 +699,40 @@ __global__ __launch_bounds__(64 * B6R_WAVES) void w4a4_bf6_splitk_reduce_kernel(
 }
 
 bool gemm_bf6_small_tiles(int M, int N, int K);
+int gemm_bf6_small_shape(int M, int N, int K, int nsplit);
+
+// One launch of the small kernel of shape (UA, UB); nsplit > 1 only on 128 x 128.
+template <int EPI, int LR, int UA, int UB, int NST = B6S_STAGES>
+static hipError_t launch_small(const uint8_t* A6, const uint8_t* W6, const float* xs, const float* ws,
+                               const void* bias, int bias_dt, void* out, int M, int N, int K, const LoraArgs& la,
+                               int nsplit, float* part, unsigned* cnt, int dev, hipStream_t st) {
+    using S = B6Small<UA, UB, NST>;
+    const int sm = (M + S::BM - 1) / S::BM;
+    const int sn = (N + S::BN - 1) / S::BN;
+    if (nsplit <= 1) {
+        static std::atomic<bool> attr[kMaxDev];
+        const hipError_t e = lds_limit_once(
+                attr, dev, reinterpret_cast<const void*>(&w4a4_gemm_bf6_small_kernel<EPI, LR, false, UA, UB, NST>),
+                S::LDS_BYTES);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((w4a4_gemm_bf6_small_kernel<EPI, LR, false, UA, UB, NST>), dim3(sm * sn), dim3(S::THREADS),
+                           S::LDS_BYTES, st, A6, W6, xs, ws, bias, bias_dt, out, M, N, K, la, tile_group_rows(sm), 1,
+                           nullptr, nullptr);
+        return hipGetLastError();
+    }
+    if constexpr (UA == 2 && UB == 2 && NST == B6S_STAGES) {
+        static std::atomic<bool> attr[kMaxDev];
+        const hipError_t e = lds_limit_once(
+                attr, dev, reinterpret_cast<const void*>(&w4a4_gemm_bf6_small_kernel<EPI, LR, true, 2, 2, B6S_STAGES>),
+                S::LDS_BYTES);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((w4a4_gemm_bf6_small_kernel<EPI, LR, true, 2, 2, B6S_STAGES>), dim3(sm * sn * nsplit),
+                           dim3(S::THREADS), S::LDS_BYTES, st, A6, W6, xs, ws, bias, bias_dt, out, M, N, K, la,
+                           tile_group_rows(sm), nsplit, part, cnt);
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
+}
 
 // Every split workspace starts with the counters of the quarter-tile kernel's
 // split (B6S_MAX_SPLIT_TILES of them, kSplitCounterBytes); the partials follow.
@@ -687,27 +754,11 @@ static hipError_t launch_bf6(const uint8_t* A6, const uint8_t* W6, const float* 
         part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(part) + kSplitCounterBytes);
     }
     if (gemm_bf6_small_tiles(M, N, K)) {
-        const int sm = (M + B6S_BM - 1) / B6S_BM;
-        const int sn = (N + B6S_BN - 1) / B6S_BN;
-        if (nsplit <= 1) {
-            static std::atomic<bool> attr_small[kMaxDev];
-            e = lds_limit_once(attr_small, dev,
-                               reinterpret_cast<const void*>(&w4a4_gemm_bf6_small_kernel<EPI, LR, false>),
-                               B6S_LDS_BYTES);
-            if (e != hipSuccess) return e;
-            hipLaunchKernelGGL((w4a4_gemm_bf6_small_kernel<EPI, LR, false>), dim3(sm * sn), dim3(B6S_THREADS),
-                               B6S_LDS_BYTES, st, A6, W6, xs, ws, bias, bias_dt, out, M, N, K, la,
-                               tile_group_rows(sm), 1, nullptr, nullptr);
-            return hipGetLastError();
-        }
-        static std::atomic<bool> attr_small_split[kMaxDev];
-        e = lds_limit_once(attr_small_split, dev,
-                           reinterpret_cast<const void*>(&w4a4_gemm_bf6_small_kernel<EPI, LR, true>), B6S_LDS_BYTES);
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((w4a4_gemm_bf6_small_kernel<EPI, LR, true>), dim3(sm * sn * nsplit), dim3(B6S_THREADS),
-                           B6S_LDS_BYTES, st, A6, W6, xs, ws, bias, bias_dt, out, M, N, K, la, tile_group_rows(sm),
-                           nsplit, part, cnt);
-        return hipGetLastError();
+        if (gemm_bf6_small_shape(M, N, K, nsplit) == SMALL_128x192)
+            return launch_small<EPI, LR, 2, 3, B6S_STAGES_192>(A6, W6, xs, ws, bias, bias_dt, out, M, N, K, la, nsplit,
+                                                               part, cnt, dev, st);
+        return launch_small<EPI, LR, 2, 2>(A6, W6, xs, ws, bias, bias_dt, out, M, N, K, la, nsplit, part, cnt, dev,
+                                           st);
     }
     const int tiles_m = (M + B6_BM - 1) / B6_BM;
     const int ntiles = tiles_m * ((N + B6_BN - 1) / B6_BN);
@@ -804,6 +855,32 @@ hipError_t gemm_bf6_launch(const void* A6, const void* W6, const float* xs, cons
 bool gemm_bf6_small_tiles(int M, int N, int K) {
     const long long tiles = (long long)((M + B6S_BM - 1) / B6S_BM) * ((N + B6S_BN - 1) / B6S_BN);
     return tiles <= B6S_MAX_SPLIT_TILES && (K <= 4096 || tiles <= 192);
+}
+
+// Tile shape of a small-kernel launch.  Splits run on 128 x 128.  Otherwise
+// 128 x 192 when its grid covers the CUs once and the 128 x 128 grid does not
+// (more than 256 tiles put two workgroups on some CUs); every other grid keeps
+// 128 x 128.  Measured on MI355X (bursts of launches, bf16 out, K = 3072, us,
+// 128 x 128 / 128 x 192 with 4 stages): 512 -> 9216 17.9 / 16.2, 512 -> 12288
+// 19.5 / 17.4, 768 -> 6144 17.6 / 16.0, 1024 -> 6144 19.1 / 17.2, 1536 -> 3072
+// 17.5 / 15.8, 2048 -> 3072 18.7 / 17.0; where 128 x 128 fits the CUs (512 ->
+// 3072 12.9 / 15.0, 512 -> 6144 13.5 / 15.6) or 128 x 192 does not (512 x 3840
+// -> 15360 25.9 / 35.5, 768 -> 9216 20.1 / 29.5) the 128 x 128 tile wins.  A
+// 64 x 128 tile (2 waves) costs as much per 128-k block as 128 x 128 with 2 to
+// 4 stages and never won.
+int gemm_bf6_small_shape(int M, int N, int K, int nsplit) {
+    (void)K;
+    if (nsplit > 1) return SMALL_128x128;
+    const long long tm = (M + 127) / 128;
+    const long long t128 = tm * ((N + 127) / 128), t192 = tm * ((N + 191) / 192);
+    return t128 > 256 && t192 <= 256 ? SMALL_128x192 : SMALL_128x128;
+}
+
+// The workgroup tile (rows of A x rows of B) of a bf6 GEMM launch.
+void gemm_bf6_tile(int M, int N, int K, int nsplit, int* bm, int* bn) {
+    if (!gemm_bf6_small_tiles(M, N, K)) { *bm = B6_BM; *bn = B6_BN; return; }
+    *bm = 128;
+    *bn = gemm_bf6_small_shape(M, N, K, nsplit) == SMALL_128x192 ? 192 : 128;
 }
 
 // Splits of the quarter-tile kernel.  Its launch costs about 5.5 us however

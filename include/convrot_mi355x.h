@@ -226,6 +226,13 @@ int cr_int4_convrot_gemm_bf6_splitk(const void* A6, const void* W6, const void* 
 /* The library's k-split count for an M x N x K bf6 GEMM (1 = no split). */
 int cr_gemm_bf6_choose_nsplit(int M, int N, int K);
 
+/* The workgroup tile (*bm rows of A x *bn rows of B) of a bf6 GEMM launch of
+ * M x N x K split nsplit ways: 256 x 256 on large grids, 128 x 128 or 128 x 192
+ * on small ones (the outputs are the same bits whichever runs).  0, or -1 for
+ * arguments no launch accepts.  No counterpart in the reference: for tests and
+ * measurement reports that name the kernel which ran. */
+int cr_gemm_bf6_tile(int M, int N, int K, int nsplit, int* bm, int* bn);
+
 /* Workspace bytes of cr_int4_convrot_gemm_bf6_splitk: 2048 counter bytes plus
  * nsplit * (256 x 256 tiles) * 256 KB (0 when nsplit == 1). */
 size_t cr_gemm_bf6_splitk_workspace(int M, int N, int nsplit);

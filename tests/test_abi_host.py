@@ -92,7 +92,7 @@ def test_load_refuses_other_abi_version(native, monkeypatch):
 
 def test_library_queries_without_gpu(native):
     lib = native.load_library()
-    assert lib.cr_abi_version() == native.ABI_VERSION == 12
+    assert lib.cr_abi_version() == native.ABI_VERSION == 13
     assert lib.cr_max_quant_k() == 32768
     assert lib.cr_max_quant_bf6_k() == 32768
 
@@ -303,6 +303,30 @@ def test_split_choice_and_workspace(native):
     assert lib.cr_gemm_bf6_splitk_workspace(512, 3072, 4) == 2048 + 4 * 24 * 256 * 256 * 4
     assert lib.cr_gemm_bf6_splitk_workspace(300, 300, 2) == 2048 + 2 * 4 * 256 * 256 * 4
     assert lib.cr_gemm_bf6_splitk_workspace(300, 300, 1) == 0
+
+
+def test_tile_choice(native):
+    """The workgroup tile is host arithmetic: 256 x 256 on large grids;
+    on small grids 128 x 192 exactly when 128 x 128 tiles exceed the 256 CUs
+    and 128 x 192 tiles do not (splits always on 128 x 128); bad arguments
+    are refused."""
+    tile = native.gemm_tile_bf6
+    assert tile(4608, 3072, 3072) == (256, 256)
+    assert tile(512, 3072, 3072) == (128, 128)                # 96 quarter tiles
+    assert tile(1024, 3072, 3072) == (128, 128)               # 192
+    assert tile(512, 9216, 3072) == (128, 192)                # 288 -> 192
+    assert tile(512, 12288, 3072) == (128, 192)               # 384 -> 256
+    assert tile(2048, 3072, 3072) == (128, 192)               # 384 -> 256
+    assert tile(512, 15360, 3840) == (128, 128)               # 480 -> 320: both exceed the CUs
+    assert tile(768, 9216, 3072) == (128, 128)                # 432 -> 288
+    assert tile(9000, 449, 1024) == (128, 192)                # 284 -> 213, ragged, edge units clamped
+    assert tile(512, 12288, 3072, nsplit=2) == (128, 128)     # splits run on the quarter tile
+    assert tile(512, 3072, 12288, nsplit=native.choose_nsplit_bf6(512, 3072, 12288)) == (128, 128)
+    lib = native.load_library()
+    bm, bn = ctypes.c_int(0), ctypes.c_int(0)
+    for args in [(0, 1, 128, 1), (1, 1, 100, 1), (1, 1, 128, 2), (1, 1, 128, 0)]:
+        assert lib.cr_gemm_bf6_tile(*args, ctypes.byref(bm), ctypes.byref(bn)) == -1, args
+    assert lib.cr_gemm_bf6_tile(1, 1, 128, 1, None, None) == -1
 
 
 def test_ops_meta_skeleton(ops_mod):

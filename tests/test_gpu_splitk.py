@@ -99,3 +99,51 @@ def test_split_counters_left_zero(native, gpu):
         first[key] = out
         wsb = native._workspaces[(torch.cuda.current_device(), st)]
         assert int(wsb[:native.SPLIT_COUNTER_BYTES].count_nonzero()) == 0, key
+
+
+# Small grids whose 128 x 128 tiles exceed the CUs run 128 x 192 tiles (6 waves,
+# 64-row operand units): full tiles, ragged M and N, and an edge tile whose last
+# B unit lies past the padded rows (9000 x 449: units re-read the last one).
+WIDE_CASES = [(512, 12288, 3072), (2048, 3072, 3072), (500, 9000, 1024), (9000, 449, 1024)]
+
+
+@pytest.mark.parametrize("M,N,K", WIDE_CASES)
+def test_wide_small_tile_acc_exact(native, oracle, gpu, M, N, K):
+    print(f"128x192 acc M={M} N={N} K={K}", flush=True)
+    assert native.gemm_tile_bf6(M, N, K) == (128, 192)
+    xp, wp, a6, w6, *_ = operands(native, M, N, K, 3 * M + N)
+    acc = native.int4_gemm_acc_bf6(a6, w6, M, N, nsplit=1)
+    rs = np.random.RandomState(M + N)
+    rows = np.unique(np.concatenate([rs.choice(M, 20, replace=False), [0, M - 1]]))
+    cols = np.unique(np.concatenate([rs.choice(N, min(N, 400), replace=False), [0, N - 1]]))
+    ref = oracle.int_gemm(xp[rows], wp[cols])
+    assert np.array_equal(acc.cpu().numpy()[np.ix_(rows, cols)], ref)
+    assert torch.equal(acc, native.int4_gemm_acc_bf6(a6, w6, M, N, nsplit=2))   # 128 x 128, split
+
+
+@pytest.mark.parametrize("M,N,K", WIDE_CASES)
+def test_wide_small_tile_epilogues_match_quarter_tiles(native, gpu, M, N, K):
+    """Every epilogue, with and without bias, equals the 128 x 128 kernel's
+    bits (its split form, which equals its unsplit form)."""
+    print(f"128x192 epilogues M={M} N={N} K={K}", flush=True)
+    _, _, a6, w6, xs, ws, b = operands(native, M, N, K, M + 5 * N)
+    for epi in (native.EPI_F32, native.EPI_BF16, native.EPI_BF16_EAGER):
+        for bias in (b, None):
+            out = native.int4_convrot_gemm_bf6(a6, w6, xs, ws, bias, epi, nsplit=1)
+            ref = native.int4_convrot_gemm_bf6(a6, w6, xs, ws, bias, epi, nsplit=2)
+            assert torch.equal(out.view(torch.int16) if out.dtype == torch.bfloat16 else out.view(torch.int32),
+                               ref.view(torch.int16) if ref.dtype == torch.bfloat16 else ref.view(torch.int32)), epi
+
+
+@pytest.mark.parametrize("R", [32, 64, 128])
+def test_wide_small_tile_lora_matches_quarter_tiles(native, gpu, R):
+    M, N, K = 500, 9000, 1024
+    assert native.gemm_tile_bf6(M, N, K) == (128, 192)
+    _, _, a6, w6, xs, ws, b = operands(native, M, N, K, R + 1)
+    g = torch.Generator(device="cuda").manual_seed(R)
+    t = torch.randn((M, R), generator=g, device="cuda").to(torch.bfloat16)
+    U = (torch.randn((N, R), generator=g, device="cuda") * 0.1).to(torch.bfloat16)
+    for epi in (native.EPI_F32, native.EPI_BF16, native.EPI_BF16_EAGER):
+        out = native.int4_convrot_gemm_bf6_lora(a6, w6, xs, ws, b, t, U, 0.75, epi, nsplit=1)
+        ref = native.int4_convrot_gemm_bf6_lora(a6, w6, xs, ws, b, t, U, 0.75, epi, nsplit=2)
+        assert torch.equal(out, ref), (epi, R)
