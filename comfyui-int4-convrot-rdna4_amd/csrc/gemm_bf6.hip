@@ -424,8 +424,8 @@ __global__ __launch_bounds__(B6_THREADS) void w4a4_gemm_bf6_kernel(
 // phase B: the first part of block kb+NST).  Same accumulators, same epilogue: the
 // outputs equal the 256 x 256 kernel's bit for bit.
 //
-// SPLIT (S = nsplit > 1, the 128 x 128 shape only): workgroup b takes tile
-// b % T and the 128-k blocks [s nkb / S, (s + 1) nkb / S) of split s = b / T.
+// SPLIT (S = nsplit > 1): workgroup b takes tile b % T and the 128-k blocks
+// [s nkb / S, (s + 1) nkb / S) of split s = b / T.
 // Every workgroup stores its raw accumulators (exact integers in fp32) in the
 // workspace with device-scope stores, waits until they are done and takes a
 // ticket from the tile's counter; the one that draws the last ticket adds the
@@ -439,8 +439,7 @@ constexpr int B6S_UNIT = 6144;                                  // 64 rows of a 
 constexpr int B6S_UNIT_Q = 4096;                                // Q part inside a unit
 constexpr int B6S_STAGES = 3;                                   // 128 x 128: 4 and 6 measured no faster
 constexpr int B6S_MAX_SPLIT_TILES = 512;                        // split counters per workspace
-constexpr int B6S_BM = 128, B6S_BN = 128;                       // the split shape
-constexpr int B6S_PART_FLOATS = B6S_BM * B6S_BN;                // one split tile's partial: 64 KB
+constexpr int B6S_BM = 128, B6S_BN = 128;                       // the quarter tile
 
 template <int UA, int UB, int NST_ = B6S_STAGES>
 struct B6Small {
@@ -459,7 +458,7 @@ struct B6Small {
     static_assert((NST - 2) * LOADS + LOADS_B <= 63 && NST >= 3, "vmcnt range");
     static_assert(BM <= 256 && BN <= 256 && THREADS >= BM && THREADS >= BN, "staged scales");
 };
-static_assert(B6Small<2, 2>::BM == B6S_BM && B6Small<2, 2>::BN == B6S_BN, "split shape");
+static_assert(B6Small<2, 2>::BM == B6S_BM && B6Small<2, 2>::BN == B6S_BN, "quarter tile");
 
 // tile shapes of the small kernel (gemm_bf6_small_shape)
 enum : int { SMALL_128x128 = 0, SMALL_128x192 = 1 };
@@ -472,7 +471,6 @@ __global__ __launch_bounds__(64 * UA * UB) void w4a4_gemm_bf6_small_kernel(
         void* __restrict__ out, int M, int N, int K, LoraArgs lora, int gm, int nsplit,
         float* __restrict__ part, unsigned* __restrict__ cnt) {
     using S = B6Small<UA, UB, NSTAGES>;
-    static_assert(!SPLIT || (UA == 2 && UB == 2), "the split runs on the 128 x 128 shape");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds6[];
 
     const int tid = threadIdx.x;
@@ -616,7 +614,7 @@ __global__ __launch_bounds__(64 * UA * UB) void w4a4_gemm_bf6_small_kernel(
     __syncthreads();                                          // every wave is done with the stages
     if constexpr (SPLIT) {
         // Partial of split s: value q (0..63) of a lane is acc[q / 32][(q / 16) % 2][q % 16], at
-        // part[((s T + tile) 4 + wave) 4096 + q 64 + lane].  Written and read with device-scope
+        // part[((s T + tile) WAVES + wave) 4096 + q 64 + lane].  Written and read with device-scope
         // relaxed atomic accesses (coherent across the XCDs' L2 caches without writing an L2 back);
         // each wave's vmcnt(0) before the barrier orders its stores before the ticket.
         const int T = tiles_m * tiles_n;
@@ -701,7 +699,7 @@ __global__ __launch_bounds__(64 * B6R_WAVES) void w4a4_bf6_splitk_reduce_kernel(
 bool gemm_bf6_small_tiles(int M, int N, int K);
 int gemm_bf6_small_shape(int M, int N, int K, int nsplit);
 
-// One launch of the small kernel of shape (UA, UB); nsplit > 1 only on 128 x 128.
+// One launch of the small kernel of shape (UA, UB) with NST stages, split nsplit ways.
 template <int EPI, int LR, int UA, int UB, int NST = B6S_STAGES>
 static hipError_t launch_small(const uint8_t* A6, const uint8_t* W6, const float* xs, const float* ws,
                                const void* bias, int bias_dt, void* out, int M, int N, int K, const LoraArgs& la,
@@ -720,18 +718,17 @@ static hipError_t launch_small(const uint8_t* A6, const uint8_t* W6, const float
                            nullptr, nullptr);
         return hipGetLastError();
     }
-    if constexpr (UA == 2 && UB == 2 && NST == B6S_STAGES) {
+    {
         static std::atomic<bool> attr[kMaxDev];
         const hipError_t e = lds_limit_once(
-                attr, dev, reinterpret_cast<const void*>(&w4a4_gemm_bf6_small_kernel<EPI, LR, true, 2, 2, B6S_STAGES>),
+                attr, dev, reinterpret_cast<const void*>(&w4a4_gemm_bf6_small_kernel<EPI, LR, true, UA, UB, NST>),
                 S::LDS_BYTES);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((w4a4_gemm_bf6_small_kernel<EPI, LR, true, 2, 2, B6S_STAGES>), dim3(sm * sn * nsplit),
+        hipLaunchKernelGGL((w4a4_gemm_bf6_small_kernel<EPI, LR, true, UA, UB, NST>), dim3(sm * sn * nsplit),
                            dim3(S::THREADS), S::LDS_BYTES, st, A6, W6, xs, ws, bias, bias_dt, out, M, N, K, la,
                            tile_group_rows(sm), nsplit, part, cnt);
         return hipGetLastError();
     }
-    return hipErrorInvalidValue;
 }
 
 // Every split workspace starts with the counters of the quarter-tile kernel's
@@ -857,22 +854,22 @@ bool gemm_bf6_small_tiles(int M, int N, int K) {
     return tiles <= B6S_MAX_SPLIT_TILES && (K <= 4096 || tiles <= 192);
 }
 
-// Tile shape of a small-kernel launch.  Splits run on 128 x 128.  Otherwise
-// 128 x 192 when its grid covers the CUs once and the 128 x 128 grid does not
-// (more than 256 tiles put two workgroups on some CUs); every other grid keeps
-// 128 x 128.  Measured on MI355X (bursts of launches, bf16 out, K = 3072, us,
-// 128 x 128 / 128 x 192 with 4 stages): 512 -> 9216 17.9 / 16.2, 512 -> 12288
-// 19.5 / 17.4, 768 -> 6144 17.6 / 16.0, 1024 -> 6144 19.1 / 17.2, 1536 -> 3072
-// 17.5 / 15.8, 2048 -> 3072 18.7 / 17.0; where 128 x 128 fits the CUs (512 ->
-// 3072 12.9 / 15.0, 512 -> 6144 13.5 / 15.6) or 128 x 192 does not (512 x 3840
-// -> 15360 25.9 / 35.5, 768 -> 9216 20.1 / 29.5) the 128 x 128 tile wins.  A
-// 64 x 128 tile (2 waves) costs as much per 128-k block as 128 x 128 with 2 to
-// 4 stages and never won.
+// Tile shape of a small-kernel launch: 128 x 192 when its grid covers the CUs
+// once (split workgroups included) and the 128 x 128 one does not (more than
+// 256 workgroups put two on some CUs); otherwise 128 x 128.  Measured on
+// MI355X (bursts of launches, bf16 out, us, 128 x 128 / 128 x 192 with 4
+// stages), K = 3072: 512 -> 9216 17.9 / 16.2, 512 -> 12288 19.5 / 17.4, 768 ->
+// 6144 17.6 / 16.0, 1024 -> 6144 19.1 / 17.2, 1536 -> 3072 17.5 / 15.8, 2048
+// -> 3072 18.7 / 17.0; where 128 x 128 fits the CUs (512 -> 3072 12.9 / 15.0,
+// 512 -> 6144 13.5 / 15.6) or 128 x 192 does not (512 x 3840 -> 15360 25.9 /
+// 35.5, 768 -> 9216 20.1 / 29.5) the 128 x 128 tile wins.  Split in two, K =
+// 12288: 1024 -> 3072 37.9 / 35.9, 768 -> 3072 35.1 / 32.1, 512 -> 6144 38.1 /
+// 35.6.  A 64 x 128 tile (2 waves) costs as much per 128-k block as 128 x 128
+// with 2 to 4 stages and never won.
 int gemm_bf6_small_shape(int M, int N, int K, int nsplit) {
     (void)K;
-    if (nsplit > 1) return SMALL_128x128;
     const long long tm = (M + 127) / 128;
-    const long long t128 = tm * ((N + 127) / 128), t192 = tm * ((N + 191) / 192);
+    const long long t128 = tm * ((N + 127) / 128) * nsplit, t192 = tm * ((N + 191) / 192) * nsplit;
     return t128 > 256 && t192 <= 256 ? SMALL_128x192 : SMALL_128x128;
 }
 
@@ -892,13 +889,18 @@ void gemm_bf6_tile(int M, int N, int K, int nsplit, int* bm, int* bn) {
 // that leaves CUs free: measured at 512 x K -> 3072 (96 tiles), K = 3072
 // 13.7 us unsplit / 13.9 split in two, K = 6144 22.0 / 18.5, K = 12288 38.9 /
 // 27.4 (S = 4: 27.5); 1024 x 12288 -> 3072 (192 tiles) 44.0 / 39.3; at
-// K = 3072 no split won on any of 15 shapes.
+// K = 3072 no split won on any of 15 shapes.  Grids of 129 to 192 quarter
+// tiles split in two run on 128 x 192 tiles (at most 256 workgroups, see
+// gemm_bf6_small_shape), and only for rows of 64 blocks or more: 1024 x 6144
+// -> 3072 runs 22.2 us unsplit against 23.6 split on 128 x 192 (24.3 on 128 x
+// 128).
 static int small_nsplit(int M, int N, int K) {
     const int T = ((M + B6S_BM - 1) / B6S_BM) * ((N + B6S_BN - 1) / B6S_BN);
     const int nkb = K / 128;
     if (nkb < 48) return 1;
     if (T <= 64 && nkb >= 96) return 4;
-    return T <= 192 ? 2 : 1;
+    if (T <= 128) return 2;
+    return T <= 192 && nkb >= 64 ? 2 : 1;     // split in two on 128 x 192 tiles
 }
 
 int gemm_bf6_choose_nsplit(int M, int N, int K) {
@@ -921,15 +923,15 @@ int gemm_bf6_choose_nsplit(int M, int N, int K) {
     return bc < 0.92 * c1 ? best : 1;
 }
 
-// The counters, then the larger of the two kernels' partials (a quarter-tile
-// grid has at most four times the tiles of the full-tile one, at a quarter of
-// the bytes each).
+// The counters, then the largest of the three tile shapes' partials (one f32
+// per output of every tile and split).
 size_t gemm_bf6_splitk_workspace(int M, int N, int nsplit) {
-    const size_t tiles = (size_t)((M + B6_BM - 1) / B6_BM) * ((N + B6_BN - 1) / B6_BN);
-    const size_t qtiles = (size_t)((M + B6S_BM - 1) / B6S_BM) * ((N + B6S_BN - 1) / B6S_BN);
-    const size_t full = (size_t)nsplit * tiles * 8 * 8192 * sizeof(float);
-    const size_t small = (size_t)nsplit * qtiles * B6S_PART_FLOATS * sizeof(float);
-    return nsplit <= 1 ? 0 : kSplitCounterBytes + (full > small ? full : small);
+    auto part_bytes = [&](int bm, int bn) {
+        return (size_t)nsplit * ((M + bm - 1) / bm) * ((N + bn - 1) / bn) * (size_t)bm * bn * sizeof(float);
+    };
+    const size_t full = part_bytes(B6_BM, B6_BN), q = part_bytes(128, 128), w = part_bytes(128, 192);
+    const size_t most = full > q ? (full > w ? full : w) : (q > w ? q : w);
+    return nsplit <= 1 ? 0 : kSplitCounterBytes + most;
 }
 
 }  // namespace convrot

@@ -203,8 +203,8 @@ int cr_int4_convrot_gemm_bf6_lora(const void* A6, const void* W6, const void* xs
 /*
  * Split-K form of the bf6 GEMM for small tile grids (few rows, large K): S
  * workgroups per output tile each take 1/S of the 128-k blocks and store their
- * raw accumulators (exact integers) in `workspace`.  On grids of 128 x 128
- * tiles the split that finishes last sums the S partials in the same kernel
+ * raw accumulators (exact integers) in `workspace`.  On grids of 128 x 128 or
+ * 128 x 192 tiles the split that finishes last sums the S partials in the same kernel
  * (a ticket from the tile's counter in the workspace's counter region decides
  * which); on 256 x 256 tiles a second kernel sums them.  Integer partials sum
  * exactly in any order, so the outputs are bit-identical to
@@ -234,7 +234,9 @@ int cr_gemm_bf6_choose_nsplit(int M, int N, int K);
 int cr_gemm_bf6_tile(int M, int N, int K, int nsplit, int* bm, int* bn);
 
 /* Workspace bytes of cr_int4_convrot_gemm_bf6_splitk: 2048 counter bytes plus
- * nsplit * (256 x 256 tiles) * 256 KB (0 when nsplit == 1). */
+ * one f32 per output of every tile and split for the largest of the tile
+ * shapes (nsplit * tiles * bm * bn * 4 over 256 x 256, 128 x 128, 128 x 192;
+ * 0 when nsplit == 1). */
 size_t cr_gemm_bf6_splitk_workspace(int M, int N, int nsplit);
 
 /*

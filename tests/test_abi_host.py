@@ -306,10 +306,10 @@ def test_split_choice_and_workspace(native):
 
 
 def test_tile_choice(native):
-    """The workgroup tile is host arithmetic: 256 x 256 on large grids;
-    on small grids 128 x 192 exactly when 128 x 128 tiles exceed the 256 CUs
-    and 128 x 192 tiles do not (splits always on 128 x 128); bad arguments
-    are refused."""
+    """The workgroup tile and the split count are host arithmetic: 256 x 256
+    on large grids; on small grids 128 x 192 exactly when 128 x 128 tiles
+    (times the splits) exceed the 256 CUs and 128 x 192 tiles do not; bad
+    arguments are refused."""
     tile = native.gemm_tile_bf6
     assert tile(4608, 3072, 3072) == (256, 256)
     assert tile(512, 3072, 3072) == (128, 128)                # 96 quarter tiles
@@ -320,8 +320,16 @@ def test_tile_choice(native):
     assert tile(512, 15360, 3840) == (128, 128)               # 480 -> 320: both exceed the CUs
     assert tile(768, 9216, 3072) == (128, 128)                # 432 -> 288
     assert tile(9000, 449, 1024) == (128, 192)                # 284 -> 213, ragged, edge units clamped
-    assert tile(512, 12288, 3072, nsplit=2) == (128, 128)     # splits run on the quarter tile
-    assert tile(512, 3072, 12288, nsplit=native.choose_nsplit_bf6(512, 3072, 12288)) == (128, 128)
+    assert tile(512, 12288, 3072, nsplit=2) == (128, 128)     # 768 split workgroups -> 512: neither fits
+    assert tile(512, 3072, 12288, nsplit=2) == (128, 128)     # 192 split workgroups
+    assert native.choose_nsplit_bf6(512, 3072, 12288) == 2
+    assert native.choose_nsplit_bf6(1024, 3072, 12288) == 2   # 192 quarter tiles, long rows:
+    assert tile(1024, 3072, 12288, nsplit=2) == (128, 192)    # 384 split workgroups -> 256
+    assert native.choose_nsplit_bf6(768, 3072, 12288) == 2
+    assert tile(768, 3072, 12288, nsplit=2) == (128, 192)
+    assert native.choose_nsplit_bf6(1024, 3072, 6144) == 1    # 48 blocks: a split of 192 tiles does not pay
+    assert native.choose_nsplit_bf6(256, 3072, 12288) == 4
+    assert tile(256, 3072, 12288, nsplit=4) == (128, 128)
     lib = native.load_library()
     bm, bn = ctypes.c_int(0), ctypes.c_int(0)
     for args in [(0, 1, 128, 1), (1, 1, 100, 1), (1, 1, 128, 2), (1, 1, 128, 0)]:

@@ -147,3 +147,31 @@ def test_wide_small_tile_lora_matches_quarter_tiles(native, gpu, R):
         out = native.int4_convrot_gemm_bf6_lora(a6, w6, xs, ws, b, t, U, 0.75, epi, nsplit=1)
         ref = native.int4_convrot_gemm_bf6_lora(a6, w6, xs, ws, b, t, U, 0.75, epi, nsplit=2)
         assert torch.equal(out, ref), (epi, R)
+
+
+# k-split on 128 x 192 tiles (grids whose split quarter tiles would exceed the
+# CUs), full and ragged, one with the last B unit past the padded rows
+WIDE_SPLIT_CASES = [(1024, 3072, 3072, 2), (1000, 3000, 8192, 2), (5000, 449, 2048, 2)]
+
+
+@pytest.mark.parametrize("M,N,K,s", WIDE_SPLIT_CASES)
+def test_wide_small_tile_split_exact(native, oracle, gpu, M, N, K, s):
+    print(f"128x192 split {s} M={M} N={N} K={K}", flush=True)
+    assert native.gemm_tile_bf6(M, N, K, s) == (128, 192)
+    xp, wp, a6, w6, xs, ws, b = operands(native, M, N, K, M + N + s)
+    acc = native.int4_gemm_acc_bf6(a6, w6, M, N, nsplit=s)
+    rs = np.random.RandomState(K)
+    rows = np.unique(np.concatenate([rs.choice(M, 16, replace=False), [0, M - 1]]))
+    assert np.array_equal(acc.cpu().numpy()[rows], oracle.int_gemm(xp[rows], wp))
+    assert torch.equal(acc, native.int4_gemm_acc_bf6(a6, w6, M, N, nsplit=1))
+    for epi in (native.EPI_F32, native.EPI_BF16, native.EPI_BF16_EAGER):
+        out = native.int4_convrot_gemm_bf6(a6, w6, xs, ws, b, epi, nsplit=s)
+        ref = native.int4_convrot_gemm_bf6(a6, w6, xs, ws, b, epi, nsplit=1)
+        assert torch.equal(out.view(torch.int16) if out.dtype == torch.bfloat16 else out.view(torch.int32),
+                           ref.view(torch.int16) if ref.dtype == torch.bfloat16 else ref.view(torch.int32)), epi
+    g = torch.Generator(device="cuda").manual_seed(s)
+    t = torch.randn((M, 32), generator=g, device="cuda").to(torch.bfloat16)
+    U = (torch.randn((N, 32), generator=g, device="cuda") * 0.1).to(torch.bfloat16)
+    out = native.int4_convrot_gemm_bf6_lora(a6, w6, xs, ws, b, t, U, 0.5, native.EPI_BF16, nsplit=s)
+    ref = native.int4_convrot_gemm_bf6_lora(a6, w6, xs, ws, b, t, U, 0.5, native.EPI_BF16, nsplit=1)
+    assert torch.equal(out, ref)
