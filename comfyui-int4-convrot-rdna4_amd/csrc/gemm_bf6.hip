@@ -496,9 +496,9 @@ __global__ __launch_bounds__(64 * UA * UB) void w4a4_gemm_bf6_small_kernel(
     scr.load(xs, ws, bias, bias_dt, M, N, m0, n0, tid);
 
     // Copy j (0 .. LOADS-1) of this wave is instruction i = wave * LOADS + j of the
-    // stage's 6 UNITS: KB i % 6 (P 0..3, Q 4..5) of unit i / 6 (A units, then B
-    // units).  Per copy: its source at the split's first block, and its LDS offset
-    // inside a stage (wave-uniform).
+    // stage's 6 * UNITS: KB i % 6 (P 0..3, Q 4..5) of unit i / 6 (A units, then B
+    // units).  Per copy: this lane's source at the split's first block, and the
+    // copy's LDS offset inside a stage (wave-uniform).
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     const int last_a = ((M + 255) >> 8) * 4 - 1, last_b = ((N + 255) >> 8) * 4 - 1;   // last 64-row units
     const uint8_t* csrc[S::LOADS];
