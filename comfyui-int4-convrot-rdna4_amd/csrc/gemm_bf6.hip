@@ -648,8 +648,8 @@ __global__ __launch_bounds__(64 * UA * UB) void w4a4_gemm_bf6_small_kernel(
     int em0 = m0, en0 = n0, elane = lane;
     asm volatile("" : "+s"(M), "+s"(N), "+v"(em0), "+v"(en0), "+v"(elane));
     constexpr int SCR = S::RING_BYTES / S::WAVES;
-    epilogue_lds<EPI, 2, 2, LR, SCR>(acc, sc, out, M, N, em0, en0, em0 + wm * 64, en0 + wn * 64, elane, lora,
-                                     lds6 + wave * SCR);
+    epilogue_lds<EPI, 2, 2, LR, SCR, 8, true>(acc, sc, out, M, N, em0, en0, em0 + wm * 64, en0 + wn * 64, elane,
+                                              lora, lds6 + wave * SCR);
 }
 
 // Split-K reduce: one 256-lane workgroup per (tile, wave slot) of the main

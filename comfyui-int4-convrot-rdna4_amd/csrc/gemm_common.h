@@ -201,7 +201,7 @@ __device__ __forceinline__ void epilogue_tiles(const AccV (&acc)[FMT][FNT], cons
 // tu_lds (rank 32, bf16 output only): the workgroup tile's t rows tile_m0 ..
 // +255 and U rows tile_n0 .. +255 staged in LDS (64 bytes per row, U at
 // +16384), read there instead of from global memory.
-template <int EPI, int FMT, int FNT, int LR, int SCR_BYTES, int ASH = 8, typename AccV>
+template <int EPI, int FMT, int FNT, int LR, int SCR_BYTES, int ASH = 8, bool HOIST = false, typename AccV>
 __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const float* sc,
                                              void* __restrict__ out, int M, int N, int tile_m0, int tile_n0,
                                              int row0, int col0, int lane, const LoraArgs& la, uint8_t* scr,
@@ -256,12 +256,36 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
 #pragma unroll
         for (int j = 0; j < FNT; ++j) load_u2(j, 0, uf[j]);
     }
+    // HOIST: the lane's row scales and its columns' scales and biases (FNT column
+    // tiles x 4 quads, 8 FNT + FMT registers) are read from the staged copy up
+    // front.  The compiler keeps an LDS read behind any earlier LDS write it may
+    // alias, so reads between the scratch writes each wait out their latency,
+    // which a wave alone on its SIMD (small grids) cannot hide; kernels with two
+    // waves per SIMD and no registers to spare read them where they are used.
+    constexpr bool SCALED = EPI != EPI_ACC && EPI != EPI_ATOMIC_ACC;
+    constexpr bool HS = HOIST && SCALED;
+    float xrow[HS ? FMT : 1];
+    float4 wcol[HS ? FNT : 1][4], bcol[HS ? FNT : 1][4];
+    if constexpr (HS) {
+#pragma unroll
+        for (int i = 0; i < FMT; ++i) xrow[i] = sc[row0 - tile_m0 + i * 32 + l32];
+#pragma unroll
+        for (int j = 0; j < FNT; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int c = col0 - tile_n0 + j * 32 + 4 * h + 8 * q;
+                wcol[j][q] = *reinterpret_cast<const float4*>(sc + 256 + c);
+                bcol[j][q] = *reinterpret_cast<const float4*>(sc + 512 + c);
+            }
+    }
 #pragma unroll
     for (int i0 = 0; i0 < FMT; i0 += PT) {
 #pragma unroll
         for (int ii = 0; ii < PT; ++ii) {
             const int i = i0 + ii;
-            const float xsv = sc[row0 - tile_m0 + i * 32 + l32];
+            float xsv;
+            if constexpr (HS) xsv = xrow[i];
+            else xsv = sc[row0 - tile_m0 + i * 32 + l32];
 #pragma unroll
             for (int j = 0; j < FNT; ++j) {
                 f32x16_t lacc = (f32x16_t){0};
@@ -294,13 +318,17 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     uint8_t* dst = scr + (ii * 32 + l32) * RS + (j * 32 + 8 * q + 4 * h) * ES;
-                    // this quad's column scales and biases, read from the staged
-                    // copy each time (cheaper than holding 32 registers per tile)
                     float wq[4] = {0.f, 0.f, 0.f, 0.f}, bq[4] = {0.f, 0.f, 0.f, 0.f};
-                    if constexpr (EPI != EPI_ACC && EPI != EPI_ATOMIC_ACC) {
-                        const int c = col0 - tile_n0 + j * 32 + 4 * h + 8 * q;
-                        const float4 w4 = *reinterpret_cast<const float4*>(sc + 256 + c);
-                        const float4 b4 = *reinterpret_cast<const float4*>(sc + 512 + c);
+                    if constexpr (SCALED) {
+                        float4 w4, b4;
+                        if constexpr (HS) {
+                            w4 = wcol[j][q];
+                            b4 = bcol[j][q];
+                        } else {   // this quad's column scales and biases, read from the staged copy
+                            const int c = col0 - tile_n0 + j * 32 + 4 * h + 8 * q;
+                            w4 = *reinterpret_cast<const float4*>(sc + 256 + c);
+                            b4 = *reinterpret_cast<const float4*>(sc + 512 + c);
+                        }
                         wq[0] = w4.x; wq[1] = w4.y; wq[2] = w4.z; wq[3] = w4.w;
                         bq[0] = b4.x; bq[1] = b4.y; bq[2] = b4.z; bq[3] = b4.w;
                     }
