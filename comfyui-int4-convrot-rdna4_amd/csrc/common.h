@@ -38,7 +38,7 @@ inline hipError_t lds_limit_once(std::atomic<bool> (&done)[kMaxDev], int dev, co
 }
 
 // Bytes 0 .. 2047 of every workspace the library takes hold the split
-// counters of the bf6 GEMM's quarter-tile kernel (one per tile, at most 512):
+// counters of the bf6 GEMM's small-tile kernel (one per tile, at most 512):
 // zero when a workspace is first used and zero again after every call; no
 // other intermediate is ever written there.
 constexpr size_t kSplitCounterBytes = 2048;

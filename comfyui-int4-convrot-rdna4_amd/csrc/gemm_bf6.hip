@@ -731,7 +731,7 @@ static hipError_t launch_small(const uint8_t* A6, const uint8_t* W6, const float
     }
 }
 
-// Every split workspace starts with the counters of the quarter-tile kernel's
+// Every split workspace starts with the counters of the small-tile kernel's
 // split (B6S_MAX_SPLIT_TILES of them, kSplitCounterBytes); the partials follow.
 static_assert(B6S_MAX_SPLIT_TILES * 4 == kSplitCounterBytes, "counter region of the documented workspace layout");
 

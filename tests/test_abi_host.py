@@ -292,8 +292,8 @@ def test_ops_refuses_unknown_prequant_layout(ops_mod):
 def test_split_choice_and_workspace(native):
     """The k-split choice is host arithmetic: large tile grids never split,
     small-M / large-K products do, within 2 .. nkb; the workspace is the 2 KB
-    counter region plus S * tiles * 256 KB (the quarter-tile kernel's partials
-    never need more)."""
+    counter region plus one f32 per output of every tile and split of the
+    largest tile shape (here the 256 x 256 one's S * tiles * 256 KB)."""
     lib = native.load_library()
     assert lib.cr_gemm_bf6_choose_nsplit(4608, 3072, 3072) == 1
     assert lib.cr_gemm_bf6_choose_nsplit(4608, 12288, 3072) == 1

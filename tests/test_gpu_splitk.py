@@ -22,9 +22,11 @@ def operands(native, M, N, K, seed):
     return xp, wp, native.int4_to_bf6(cu(xp)), native.int4_to_bf6(cu(wp)), cu(xs), cu(ws), cu(b)
 
 
-# Grids of at most 512 quarter tiles take the 128 x 128 kernel, whose splits
-# are reduced in the kernel by the last split of each tile; larger grids take
-# the 256 x 256 partial kernel and the reduce kernel (the last case).
+# Grids of at most 512 quarter tiles take the small-tile kernel (128 x 128, or
+# 128 x 192 where the split quarter tiles would exceed the CUs: 1024 x 3072 in
+# two), whose splits are reduced in the kernel by the last split of each tile;
+# larger grids take the 256 x 256 partial kernel and the reduce kernel (the
+# last case).
 SPLIT_CASES = [(512, 3072, 12288, [2, 5, 6, 16, 96]), (300, 700, 1024, [2, 3, 8]), (1024, 3072, 3072, [2, 4, 24]),
                (64, 256, 256, [2]), (257, 513, 3840, [7, 30]), (640, 13312, 2048, [2, 4])]
 
