@@ -620,7 +620,9 @@ def bench_dit(args):
     MLP ratio 4; 4096 image + 512 text tokens) loaded through Int4ConvRotOps
     with the Flux 2 skip list and a rank-32 dynamic LoRA on each of its 64
     quantized linears.  One step = one forward.  Reports the forward time, the
-    GPU time inside the quantized linears (HIP events around each call), the
+    same forward captured in a HIP graph and replayed (bits checked against the
+    eager forward), the GPU time inside the quantized linears (HIP events
+    around each call), the
     same linears replayed back to back through the C-ABI's one-call linear
     (with and without the LoRA: their difference is the LoRA's cost) and the
     difference between the two: the per-layer cost of the Linear replacement's
@@ -662,6 +664,31 @@ def bench_dit(args):
         host_s = (time.perf_counter() - h0) / args.steps
         torch.cuda.synchronize()
         ms_fwd = e0.elapsed_time(e1) / args.steps
+
+        # the same forward captured once in a HIP graph and replayed: no host
+        # work per launch (the Linear replacement's Python path included); the
+        # replay's output is checked against the eager forward's bits
+        static = [img.clone(), ctx.clone(), tt.clone()]
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            model(*static)
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            gout = model(*static)
+        graph.replay()
+        eager_out = model(img, ctx, tt)
+        torch.cuda.synchronize()
+        graph_exact = bool(torch.equal(gout.view(torch.int16), eager_out.view(torch.int16)))
+        e0.record(stream)
+        for _ in range(args.steps):
+            graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms_graph = e0.elapsed_time(e1) / args.steps
+        del graph, gout, eager_out, static
 
         # GPU time inside the quantized linears: events around each call
         evs, inputs = [], {}
@@ -761,6 +788,8 @@ def bench_dit(args):
             "quantized_linears": len(qlayers),
         },
         "forward_ms": round(ms_fwd, 3),
+        "forward_graph_ms": round(ms_graph, 3),
+        "graph_replay_bit_exact": graph_exact,
         "host_ms_per_forward": round(host_s * 1e3, 3),
         "quantized_linear_ms": round(lin_ms, 3),
         "other_ms": round(ms_fwd - lin_ms, 3),
