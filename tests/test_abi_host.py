@@ -449,3 +449,37 @@ def test_too_wide_rows_stay_bf16(ops_mod, backend):
         assert any("loading it dequantized" in r.getMessage() for r in records)
     finally:
         logging.getLogger().removeHandler(handler)
+
+
+def test_split_workspace_covers_every_launch(native):
+    """Host arithmetic the kernels' memory safety rests on, over random shapes
+    and every split count a caller may pass: the workspace holds the counter
+    region plus one f32 per output of every tile and split of the tile shape
+    that launch runs, a split small-tile grid needs at most 512 counters, and
+    the one-call linear's workspace holds its split partials, B6T codes,
+    scales and t."""
+    lib = native.load_library()
+    rs = np.random.RandomState(11)
+    bm, bn = ctypes.c_int(0), ctypes.c_int(0)
+    for _ in range(400):
+        M = int(rs.choice([1, 7, 64, 255, 256, 300, 512, 1000, 1024, 2048, 4608, 9000, 16384]) + rs.randint(0, 3))
+        N = int(rs.choice([1, 64, 200, 449, 700, 3000, 3072, 9216, 12288, 13312]) + rs.randint(0, 3))
+        K = 128 * int(rs.randint(1, 120))
+        for ns in sorted({1, 2, 3, lib.cr_gemm_bf6_choose_nsplit(M, N, K), int(rs.randint(1, K // 128 + 1))}):
+            if ns > K // 128:
+                continue
+            assert lib.cr_gemm_bf6_tile(M, N, K, ns, ctypes.byref(bm), ctypes.byref(bn)) == 0
+            tiles = ((M + bm.value - 1) // bm.value) * ((N + bn.value - 1) // bn.value)
+            ws = lib.cr_gemm_bf6_splitk_workspace(M, N, ns)
+            if ns == 1:
+                assert ws == 0
+                continue
+            assert ws >= 2048 + ns * tiles * bm.value * bn.value * 4, (M, N, K, ns, bm.value, bn.value)
+            if bm.value == 128:
+                assert tiles <= 512, (M, N, K, ns)
+        for R in (0, 32):
+            need = lib.cr_convrot_w4a4_linear_bf6_workspace(M, N, K, R)
+            ns = lib.cr_gemm_bf6_choose_nsplit(M, N, K)
+            rows = (M + 255) // 256 * 256
+            floor = max(lib.cr_gemm_bf6_splitk_workspace(M, N, ns), 2048) + rows * K * 3 // 4 + 4 * M + 2 * M * R
+            assert need >= floor, (M, N, K, R)
