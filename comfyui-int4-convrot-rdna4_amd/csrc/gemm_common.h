@@ -219,6 +219,8 @@ __device__ __forceinline__ void epilogue_lds(const AccV (&acc)[FMT][FNT], const 
     constexpr int PT = 1;
     static_assert(SCR_BYTES >= 32 * RS, "scratch too small for one row tile");
     constexpr int CW = RB / 16;                      // 16-byte chunks per row
+    // the store pass maps the 64 lanes onto whole rows of 16-byte chunks
+    static_assert(64 % CW == 0, "a wave's lanes cover whole rows of the staged tile (FNT 1, 2 or 4)");
     constexpr int EPC = 16 / ES;                     // elements per chunk
     const int h = lane >> 5;
     const int l32 = lane & 31;
